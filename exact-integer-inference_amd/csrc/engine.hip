@@ -1,0 +1,666 @@
+// Host side of libeii: model.bin loading, the batched forward and the C ABI (include/eii.h).
+//
+// model.bin is the reference's file ABI (python/export_vectors.py:24-45): sequential
+// little-endian arrays, all scalars int64.  The loader narrows every field to the width the
+// semantics allow (int8 weights, 14-bit multipliers, per-row shifts, Q30 tables) and rejects
+// a file whose values do not fit, so the kernels never meet an out-of-range operand.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/eii.h"
+#include "eii_int.h"
+#include "kernels.h"
+
+using namespace eii;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const std::string& msg) {
+  g_err = msg;
+  return code;
+}
+
+#define HIPCHK(expr)                                                                        \
+  do {                                                                                      \
+    hipError_t e_ = (expr);                                                                 \
+    if (e_ != hipSuccess)                                                                   \
+      return fail(EII_E_DEVICE, std::string(#expr) + ": " + hipGetErrorString(e_));         \
+  } while (0)
+
+enum Site { NORM1 = 0, QP, KP, VP, QR, KR, CTX, NORM2, GATE, UP, SILU, GATED, NSITES };
+const char* kSiteNames[NSITES] = {"norm1_out", "q_proj", "k_proj", "v_proj", "q_rope", "k_rope",
+                                  "attn_ctx", "norm2_out", "gate_proj", "up_proj", "silu_gate", "mlp_gated"};
+const int kMatN[7] = {576, 192, 192, 576, 1536, 1536, 576};
+const int kMatK[7] = {576, 576, 576, 576, 576, 576, 1536};
+
+struct Mat {            // device arrays of one projection (possibly several matrices stacked)
+  int8_t* W = nullptr;  // [N, K]
+  int32_t* mult = nullptr;
+  int32_t* shift = nullptr;
+  int32_t* wsum = nullptr;
+  int N = 0, K = 0;
+};
+
+struct Layer {
+  int bits[NSITES], f[NSITES];
+  int64_t fm[24];
+  int f_m;               // gated exponent actually used (python/intref.py:274)
+  int32_t *ln1, *ln2;
+  int ln1_f, ln2_f;
+  Mat qkv, o, gu, down;
+  int32_t* silu;
+};
+
+// Device arena: one allocation for all model arrays.
+struct Arena {
+  std::vector<uint8_t> host;
+  size_t off = 0;
+  size_t take(size_t bytes) {
+    off = (off + 255) & ~(size_t)255;
+    size_t o = off;
+    off += bytes;
+    if (host.size() < off) host.resize(off);
+    return o;
+  }
+};
+
+}  // namespace
+
+struct eii_model {
+  int device = 0;
+  uint8_t* dev = nullptr;           // arena base
+  // header arrays (device)
+  int8_t* emb_q = nullptr;
+  int32_t *emb_m = nullptr, *emb_sh = nullptr;   // embed shift n - 15
+  Mat head;                                       // tied head: W = emb_q, shift = n + f_y - 16
+  int32_t* fg = nullptr;
+  int fg_f = 0, f_y = 0;
+  int32_t* exp_tab = nullptr;
+  int32_t *rope_c = nullptr, *rope_s = nullptr;   // [rope_rows, 32]
+  int rope_rows = 0;
+  bool rope_owned = false;
+  Layer L[kNL];
+  int64_t fy_raw = 0;
+  // workspace
+  size_t ws_rows = 0;
+  int32_t* x = nullptr;            // [M, 576]
+  void* h = nullptr;               // [M, 576] up to int32
+  int16_t* qkv = nullptr;          // [M, 960]
+  void* ctx = nullptr;             // [M, 576] up to int32
+  int16_t* gu = nullptr;           // [M, 3072]
+  void* gated = nullptr;           // [M, 1536] up to int32
+  int32_t* pos = nullptr;          // [M]
+  int32_t* seq_off = nullptr;      // [nseq + 1]
+  size_t seq_cap = 0;
+  std::vector<int32_t> last_lens;
+  int* flags = nullptr;            // [1]: 1 logit overflow, 2 token id out of range
+};
+
+namespace {
+
+// ------------------------------------------------------------------------------ loading
+struct Reader {
+  const uint8_t* p;
+  size_t n, off = 0;
+  bool ok = true;
+  const uint8_t* bytes(size_t k) {
+    if (off + k > n) { ok = false; return nullptr; }
+    const uint8_t* r = p + off;
+    off += k;
+    return r;
+  }
+  int64_t i64() {
+    const uint8_t* b = bytes(8);
+    if (!b) return 0;
+    int64_t v;
+    memcpy(&v, b, 8);
+    return v;
+  }
+  std::vector<int64_t> vec(size_t k) {
+    std::vector<int64_t> v(k);
+    const uint8_t* b = bytes(8 * k);
+    if (b) memcpy(v.data(), b, 8 * k);
+    return v;
+  }
+};
+
+bool fits32(int64_t v) { return v >= INT32_MIN && v <= INT32_MAX; }
+
+int narrow32(const std::vector<int64_t>& v, int32_t* dst, int64_t lo, int64_t hi, const std::string& what) {
+  for (size_t i = 0; i < v.size(); ++i) {
+    if (v[i] < lo || v[i] > hi)
+      return fail(EII_E_BOUND, what + "[" + std::to_string(i) + "] = " + std::to_string(v[i]) +
+                                   " outside [" + std::to_string(lo) + ", " + std::to_string(hi) + "]");
+    dst[i] = (int32_t)v[i];
+  }
+  return EII_OK;
+}
+
+int check_site(const Layer& L, int l, int s, bool allow32) {
+  const int b = L.bits[s];
+  if (!(b == 16 || (allow32 && b == 32)))
+    return fail(EII_E_BOUND, "layer " + std::to_string(l) + " site " + kSiteNames[s] + ": " +
+                                 std::to_string(b) + "-bit format is not supported here");
+  if (L.f[s] < -64 || L.f[s] > 64)
+    return fail(EII_E_BOUND, "layer " + std::to_string(l) + " site " + kSiteNames[s] + ": f out of range");
+  return EII_OK;
+}
+
+int check_scalar_shift(int sh, const std::string& what) {
+  if (sh < -30 || sh > 62) return fail(EII_E_BOUND, what + " shift " + std::to_string(sh) + " out of range");
+  return EII_OK;
+}
+
+}  // namespace
+
+extern "C" const char* eii_last_error(void) { return g_err.c_str(); }
+
+extern "C" int eii_model_load(const char* path, int device, eii_model** out) {
+  if (!path || !out) return fail(EII_E_ARG, "null argument");
+  *out = nullptr;
+  FILE* f = fopen(path, "rb");
+  if (!f) return fail(EII_E_IO, std::string(path) + ": cannot open");
+  fseek(f, 0, SEEK_END);
+  const long size = ftell(f);
+  fseek(f, 0, SEEK_SET);
+  const size_t expect = 154045048;
+  if (size != (long)expect) {
+    fclose(f);
+    return fail(EII_E_IO, std::string(path) + ": " + std::to_string(size) + " bytes, a model.bin holds " +
+                              std::to_string(expect));
+  }
+  std::vector<uint8_t> file(expect);
+  const size_t got = fread(file.data(), 1, expect, f);
+  fclose(f);
+  if (got != expect) return fail(EII_E_IO, std::string(path) + ": short read");
+
+  Reader rd{file.data(), file.size()};
+  Arena ar;
+  int rc;
+  eii_model* M = new eii_model();
+  M->device = device;
+
+  // offsets into the arena, resolved to device pointers after the upload
+  struct MatOff { size_t W, mult, shift, wsum; int N, K; };
+  size_t o_embq = ar.take((size_t)kV * kD);
+  memcpy(ar.host.data() + o_embq, rd.bytes((size_t)kV * kD), (size_t)kV * kD);
+  const std::vector<int64_t> emb_m = rd.vec(kV), emb_n = rd.vec(kV), fgq = rd.vec(kD);
+  const int64_t fg_f = rd.i64(), f_y = rd.i64();
+  const std::vector<int64_t> expt = rd.vec(kDMax + 1), rc_ = rd.vec(512 * 32), rs_ = rd.vec(512 * 32);
+  if (!rd.ok) { delete M; return fail(EII_E_IO, "short read in header"); }
+  if (fg_f < -64 || fg_f > 64 || f_y < -64 || f_y > 64) { delete M; return fail(EII_E_BOUND, "final gain/f_y exponent out of range"); }
+  M->fg_f = (int)fg_f;
+  M->f_y = (int)f_y;
+
+  size_t o_embm = ar.take(4 * kV), o_embsh = ar.take(4 * kV), o_headsh = ar.take(4 * kV), o_headws = ar.take(4 * kV);
+  size_t o_fg = ar.take(4 * kD), o_exp = ar.take(4 * (kDMax + 1)), o_rc = ar.take(4 * 512 * 32), o_rs = ar.take(4 * 512 * 32);
+  {
+    std::vector<int64_t> esh(kV), hsh(kV);
+    for (int i = 0; i < kV; ++i) { esh[i] = emb_n[i] - kFRes; hsh[i] = emb_n[i] + f_y - 16; }
+    if ((rc = narrow32(emb_m, (int32_t*)(ar.host.data() + o_embm), -(1 << 14), 1 << 14, "emb_m")) ||
+        (rc = narrow32(esh, (int32_t*)(ar.host.data() + o_embsh), 1, 62, "embedding shift emb_n - 15")) ||
+        (rc = narrow32(hsh, (int32_t*)(ar.host.data() + o_headsh), 1, 62, "head shift emb_n + f_y - 16")) ||
+        (rc = narrow32(fgq, (int32_t*)(ar.host.data() + o_fg), INT32_MIN + 1, INT32_MAX, "final gain")) ||
+        (rc = narrow32(expt, (int32_t*)(ar.host.data() + o_exp), 0, INT32_MAX, "exp table")) ||
+        (rc = narrow32(rc_, (int32_t*)(ar.host.data() + o_rc), INT32_MIN, INT32_MAX, "rope cos")) ||
+        (rc = narrow32(rs_, (int32_t*)(ar.host.data() + o_rs), INT32_MIN, INT32_MAX, "rope sin"))) {
+      delete M;
+      return rc;
+    }
+    if (expt[0] < 1) { delete M; return fail(EII_E_BOUND, "exp table entry 0 must be positive"); }
+  }
+
+  struct LayerOff { size_t ln1, ln2, silu; MatOff qkv, o, gu, down; };
+  std::vector<LayerOff> lo(kNL);
+  for (int l = 0; l < kNL; ++l) {
+    Layer& L = M->L[l];
+    for (int i = 0; i < 24; ++i) L.fm[i] = rd.i64();
+    for (int s = 0; s < NSITES; ++s) {
+      if (L.fm[2 * s] < 0 || L.fm[2 * s] > 64 || L.fm[2 * s + 1] < -64 || L.fm[2 * s + 1] > 64) {
+        delete M;
+        return fail(EII_E_BOUND, "layer " + std::to_string(l) + ": fm record out of range");
+      }
+      L.bits[s] = (int)L.fm[2 * s];
+      L.f[s] = (int)L.fm[2 * s + 1];
+    }
+    const std::vector<int64_t> ln1 = rd.vec(kD);
+    const int64_t ln1f = rd.i64();
+    const std::vector<int64_t> ln2 = rd.vec(kD);
+    const int64_t ln2f = rd.i64();
+    if (!rd.ok) { delete M; return fail(EII_E_IO, "short read in layer " + std::to_string(l)); }
+    if ((rc = check_site(L, l, NORM1, true)) || (rc = check_site(L, l, QP, false)) ||
+        (rc = check_site(L, l, KP, false)) || (rc = check_site(L, l, VP, false)) ||
+        (rc = check_site(L, l, QR, false)) || (rc = check_site(L, l, KR, false)) ||
+        (rc = check_site(L, l, CTX, true)) || (rc = check_site(L, l, NORM2, true)) ||
+        (rc = check_site(L, l, GATE, false)) || (rc = check_site(L, l, UP, false)) ||
+        (rc = check_site(L, l, SILU, true)) || (rc = check_site(L, l, GATED, true))) {
+      delete M;
+      return rc;
+    }
+    if (ln1f < -64 || ln1f > 64 || ln2f < -64 || ln2f > 64) { delete M; return fail(EII_E_BOUND, "gain exponent out of range"); }
+    L.ln1_f = (int)ln1f;
+    L.ln2_f = (int)ln2f;
+    L.f_m = L.bits[GATED] == 32 ? std::min(L.f[GATED], L.f[SILU] + L.f[UP]) : L.f[GATED];
+    const int shift_s = L.f[QR] + L.f[KR] + 3 - kFScore;
+    if (shift_s < 1) { delete M; return fail(EII_E_BOUND, "layer " + std::to_string(l) + ": score shift < 1"); }
+    if ((rc = check_scalar_shift(21 + L.ln1_f - L.f[NORM1], "norm1")) ||
+        (rc = check_scalar_shift(21 + L.ln2_f - L.f[NORM2], "norm2")) ||
+        (rc = check_scalar_shift(30 + L.f[QP] - L.f[QR], "q rope")) ||
+        (rc = check_scalar_shift(30 + L.f[KP] - L.f[KR], "k rope")) ||
+        (rc = check_scalar_shift(shift_s, "score")) ||
+        (rc = check_scalar_shift(16 + L.f[VP] - L.f[CTX], "context")) ||
+        (rc = check_scalar_shift(L.f[SILU] + L.f[UP] - L.f_m, "gated"))) {
+      delete M;
+      return rc;
+    }
+    LayerOff& O = lo[l];
+    O.ln1 = ar.take(4 * kD);
+    O.ln2 = ar.take(4 * kD);
+    if ((rc = narrow32(ln1, (int32_t*)(ar.host.data() + O.ln1), INT32_MIN + 1, INT32_MAX, "ln1")) ||
+        (rc = narrow32(ln2, (int32_t*)(ar.host.data() + O.ln2), INT32_MIN + 1, INT32_MAX, "ln2"))) {
+      delete M;
+      return rc;
+    }
+    // projections, stacked: qkv = q | k | v, gu = gate | up
+    O.qkv = {ar.take((size_t)960 * 576), ar.take(4 * 960), ar.take(4 * 960), ar.take(4 * 960), 960, 576};
+    O.o = {ar.take((size_t)576 * 576), ar.take(4 * 576), ar.take(4 * 576), ar.take(4 * 576), 576, 576};
+    O.gu = {ar.take((size_t)3072 * 576), ar.take(4 * 3072), ar.take(4 * 3072), ar.take(4 * 3072), 3072, 576};
+    O.down = {ar.take((size_t)576 * 1536), ar.take(4 * 576), ar.take(4 * 576), ar.take(4 * 576), 576, 1536};
+    // matrix i -> (stack, row offset, f_in, f_out)
+    const MatOff* dst[7] = {&O.qkv, &O.qkv, &O.qkv, &O.o, &O.gu, &O.gu, &O.down};
+    const int row0[7] = {0, 576, 768, 0, 0, 1536, 0};
+    const int fin[7] = {L.f[NORM1], L.f[NORM1], L.f[NORM1], L.f[CTX], L.f[NORM2], L.f[NORM2], L.f_m};
+    const int fout[7] = {L.f[QP], L.f[KP], L.f[VP], kFRes, L.f[GATE], L.f[UP], kFRes};
+    static const char* names[7] = {"q", "k", "v", "o", "gate", "up", "down"};
+    for (int i = 0; i < 7; ++i) {
+      const int N = kMatN[i], K = kMatK[i];
+      const uint8_t* wq = rd.bytes((size_t)N * K);
+      const std::vector<int64_t> m = rd.vec(N), n = rd.vec(N);
+      if (!rd.ok) { delete M; return fail(EII_E_IO, "short read in layer " + std::to_string(l)); }
+      memcpy(ar.host.data() + dst[i]->W + (size_t)row0[i] * K, wq, (size_t)N * K);
+      std::vector<int64_t> sh(N);
+      for (int r = 0; r < N; ++r) sh[r] = n[r] + fin[i] - fout[i];
+      const std::string what = "layer " + std::to_string(l) + " " + names[i];
+      if ((rc = narrow32(m, (int32_t*)(ar.host.data() + dst[i]->mult) + row0[i], -(1 << 14), 1 << 14, what + " m")) ||
+          (rc = narrow32(sh, (int32_t*)(ar.host.data() + dst[i]->shift) + row0[i], 1, 62, what + " requant shift"))) {
+        delete M;
+        return rc;
+      }
+    }
+    const std::vector<int64_t> silu = rd.vec(65536);
+    if (!rd.ok) { delete M; return fail(EII_E_IO, "short read in layer " + std::to_string(l)); }
+    O.silu = ar.take(4 * 65536);
+    const int bs = L.bits[SILU];
+    if ((rc = narrow32(silu, (int32_t*)(ar.host.data() + O.silu), -(1LL << (bs - 1)), (1LL << (bs - 1)) - 1,
+                       "layer " + std::to_string(l) + " silu table"))) {
+      delete M;
+      return rc;
+    }
+  }
+  if (rd.off != rd.n) { delete M; return fail(EII_E_IO, "model.bin has trailing bytes"); }
+
+  // upload
+  HIPCHK(hipSetDevice(device));
+  if (hipMalloc(&M->dev, ar.host.size()) != hipSuccess) { delete M; return fail(EII_E_DEVICE, "hipMalloc of the model failed"); }
+  if (hipMemcpy(M->dev, ar.host.data(), ar.host.size(), hipMemcpyHostToDevice) != hipSuccess) {
+    (void)hipFree(M->dev); delete M; return fail(EII_E_DEVICE, "model upload failed");
+  }
+  uint8_t* d = M->dev;
+  M->emb_q = (int8_t*)(d + o_embq);
+  M->emb_m = (int32_t*)(d + o_embm);
+  M->emb_sh = (int32_t*)(d + o_embsh);
+  M->head = {M->emb_q, M->emb_m, (int32_t*)(d + o_headsh), (int32_t*)(d + o_headws), kV, kD};
+  M->fg = (int32_t*)(d + o_fg);
+  M->exp_tab = (int32_t*)(d + o_exp);
+  M->rope_c = (int32_t*)(d + o_rc);
+  M->rope_s = (int32_t*)(d + o_rs);
+  M->rope_rows = 512;
+  auto mat = [&](const MatOff& o) {
+    return Mat{(int8_t*)(d + o.W), (int32_t*)(d + o.mult), (int32_t*)(d + o.shift), (int32_t*)(d + o.wsum), o.N, o.K};
+  };
+  for (int l = 0; l < kNL; ++l) {
+    Layer& L = M->L[l];
+    L.ln1 = (int32_t*)(d + lo[l].ln1);
+    L.ln2 = (int32_t*)(d + lo[l].ln2);
+    L.silu = (int32_t*)(d + lo[l].silu);
+    L.qkv = mat(lo[l].qkv);
+    L.o = mat(lo[l].o);
+    L.gu = mat(lo[l].gu);
+    L.down = mat(lo[l].down);
+  }
+  M->fy_raw = f_y;
+  // weight row sums for the limb bias correction
+  hipError_t e = weight_colsum(M->head.W, kV, kD, M->head.wsum, nullptr);
+  for (int l = 0; l < kNL && e == hipSuccess; ++l) {
+    Layer& L = M->L[l];
+    Mat* ms[4] = {&L.qkv, &L.o, &L.gu, &L.down};
+    for (Mat* m : ms) if (e == hipSuccess) e = weight_colsum(m->W, m->N, m->K, m->wsum, nullptr);
+  }
+  if (e == hipSuccess) e = hipMalloc(&M->flags, 16);
+  if (e == hipSuccess) e = hipMemset(M->flags, 0, 16);
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (e != hipSuccess) { eii_model_free(M); return fail(EII_E_DEVICE, std::string("model setup: ") + hipGetErrorString(e)); }
+  *out = M;
+  return EII_OK;
+}
+
+static void free_ws(eii_model* m) {
+  void* ps[] = {m->x, m->h, m->qkv, m->ctx, m->gu, m->gated, m->pos};
+  for (void* p : ps) if (p) (void)hipFree(p);
+  m->x = nullptr; m->h = nullptr; m->qkv = nullptr; m->ctx = nullptr; m->gu = nullptr; m->gated = nullptr; m->pos = nullptr;
+  m->ws_rows = 0;
+}
+
+extern "C" void eii_model_free(eii_model* m) {
+  if (!m) return;
+  hipSetDevice(m->device);
+  free_ws(m);
+  if (m->seq_off) (void)hipFree(m->seq_off);
+  if (m->rope_owned) { (void)hipFree(m->rope_c); (void)hipFree(m->rope_s); }
+  if (m->flags) (void)hipFree(m->flags);
+  if (m->dev) (void)hipFree(m->dev);
+  delete m;
+}
+
+extern "C" int eii_model_set_rope(eii_model* m, const int64_t* c, const int64_t* s, int rows) {
+  if (!m || !c || !s || rows <= 0) return fail(EII_E_ARG, "bad rope arguments");
+  std::vector<int32_t> hc((size_t)rows * 32), hs((size_t)rows * 32);
+  for (size_t i = 0; i < hc.size(); ++i) {
+    if (!fits32(c[i]) || !fits32(s[i])) return fail(EII_E_BOUND, "rope table entry outside int32");
+    hc[i] = (int32_t)c[i];
+    hs[i] = (int32_t)s[i];
+  }
+  HIPCHK(hipSetDevice(m->device));
+  int32_t *dc = nullptr, *ds = nullptr;
+  HIPCHK(hipMalloc(&dc, hc.size() * 4));
+  if (hipMalloc(&ds, hs.size() * 4) != hipSuccess) { (void)hipFree(dc); return fail(EII_E_DEVICE, "rope alloc"); }
+  HIPCHK(hipDeviceSynchronize());
+  if (hipMemcpy(dc, hc.data(), hc.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
+      hipMemcpy(ds, hs.data(), hs.size() * 4, hipMemcpyHostToDevice) != hipSuccess) {
+    (void)hipFree(dc); (void)hipFree(ds);
+    return fail(EII_E_DEVICE, "rope upload");
+  }
+  if (m->rope_owned) { (void)hipFree(m->rope_c); (void)hipFree(m->rope_s); }
+  m->rope_c = dc;
+  m->rope_s = ds;
+  m->rope_rows = rows;
+  m->rope_owned = true;
+  return EII_OK;
+}
+
+extern "C" int eii_model_rope_rows(const eii_model* m) { return m ? m->rope_rows : 0; }
+
+extern "C" int eii_model_formats(const eii_model* m, int layer, int64_t* fm24, int64_t* f_y) {
+  if (!m || layer < 0 || layer >= kNL) return fail(EII_E_ARG, "bad layer");
+  if (fm24) memcpy(fm24, m->L[layer].fm, sizeof(m->L[layer].fm));
+  if (f_y) *f_y = m->fy_raw;
+  return EII_OK;
+}
+
+// ------------------------------------------------------------------------------ forward
+namespace {
+
+int ensure_ws(eii_model* m, size_t rows) {
+  if (rows <= m->ws_rows) return EII_OK;
+  free_ws(m);
+  size_t r = rows;
+  hipError_t e = hipSuccess;
+  auto al = [&](void** p, size_t bytes) { if (e == hipSuccess) e = hipMalloc(p, bytes); };
+  al((void**)&m->x, r * kD * 4);
+  al(&m->h, r * kD * 4);
+  al((void**)&m->qkv, r * kQKVN * 2);
+  al(&m->ctx, r * kD * 4);
+  al((void**)&m->gu, r * 2 * kDFF * 2);
+  al(&m->gated, r * kDFF * 4);
+  al((void**)&m->pos, r * 4);
+  if (e != hipSuccess) { free_ws(m); return fail(EII_E_DEVICE, "workspace allocation failed"); }
+  m->ws_rows = r;
+  m->last_lens.clear();
+  return EII_OK;
+}
+
+// Uploads positions and sequence offsets for this batch shape (cached between calls).
+int set_batch(eii_model* m, const std::vector<int32_t>& lens, hipStream_t s) {
+  if (lens == m->last_lens) return EII_OK;
+  size_t rows = 0;
+  std::vector<int32_t> off(lens.size() + 1, 0), pos;
+  for (size_t i = 0; i < lens.size(); ++i) {
+    off[i + 1] = off[i] + lens[i];
+    for (int t = 0; t < lens[i]; ++t) pos.push_back(t);
+  }
+  rows = pos.size();
+  if (m->seq_cap < off.size()) {
+    if (m->seq_off) (void)hipFree(m->seq_off);
+    m->seq_off = nullptr;
+    HIPCHK(hipMalloc(&m->seq_off, off.size() * 4));
+    m->seq_cap = off.size();
+  }
+  HIPCHK(hipMemcpyAsync(m->seq_off, off.data(), off.size() * 4, hipMemcpyHostToDevice, s));
+  if (rows) HIPCHK(hipMemcpyAsync(m->pos, pos.data(), rows * 4, hipMemcpyHostToDevice, s));
+  HIPCHK(hipStreamSynchronize(s));    // the host vectors die at return
+  m->last_lens = lens;
+  return EII_OK;
+}
+
+int gemm_req(const Mat& W, const void* A, int a_bytes, int M, void* out, int out_bits, hipStream_t s) {
+  GemmArgs g{A, W.W, M, W.N, W.K, W.wsum, W.mult, W.shift, out, out_bits, nullptr};
+  HIPCHK(gemm(g, a_bytes, out_bits == 16 ? EPI_REQ16 : EPI_REQ32, s));
+  return EII_OK;
+}
+
+int gemm_resid(const Mat& W, const void* A, int a_bytes, int M, int32_t* x, hipStream_t s) {
+  GemmArgs g{A, W.W, M, W.N, W.K, W.wsum, W.mult, W.shift, x, 32, nullptr};
+  HIPCHK(gemm(g, a_bytes, EPI_RESID, s));
+  return EII_OK;
+}
+
+hipError_t copy_cols(void* dst, int dst_w, const void* src, int src_w, int col0, int ncols, int esz, int rows,
+                     hipStream_t s) {
+  return hipMemcpy2DAsync(dst, (size_t)dst_w * esz, (const uint8_t*)src + (size_t)col0 * esz, (size_t)src_w * esz,
+                          (size_t)ncols * esz, rows, hipMemcpyDeviceToDevice, s);
+}
+
+int run_block(eii_model* m, int l, int32_t* x, int M, int nseq, int max_T, const eii_trace* tr, hipStream_t s) {
+  const Layer& L = m->L[l];
+  const int hb = L.bits[NORM1] / 8;
+  HIPCHK(rmsnorm(x, M, L.ln1, 21 + L.ln1_f - L.f[NORM1], L.bits[NORM1], m->h, hb, s));
+  if (tr && tr->norm1_out) HIPCHK(hipMemcpyAsync(tr->norm1_out, m->h, (size_t)M * kD * hb, hipMemcpyDeviceToDevice, s));
+  int rc;
+  if ((rc = gemm_req(L.qkv, m->h, hb, M, m->qkv, 16, s))) return rc;
+  if (tr && tr->q_proj) HIPCHK(copy_cols(tr->q_proj, kD, m->qkv, kQKVN, 0, kD, 2, M, s));
+  if (tr && tr->k_proj) HIPCHK(copy_cols(tr->k_proj, 192, m->qkv, kQKVN, kD, 192, 2, M, s));
+  if (tr && tr->v_proj) HIPCHK(copy_cols(tr->v_proj, 192, m->qkv, kQKVN, kD + 192, 192, 2, M, s));
+  HIPCHK(rope(m->qkv, M, m->pos, m->rope_c, m->rope_s, 30 + L.f[QP] - L.f[QR], L.bits[QR], 30 + L.f[KP] - L.f[KR],
+              L.bits[KR], s));
+  if (tr && tr->q_rope) HIPCHK(copy_cols(tr->q_rope, kD, m->qkv, kQKVN, 0, kD, 2, M, s));
+  if (tr && tr->k_rope) HIPCHK(copy_cols(tr->k_rope, 192, m->qkv, kQKVN, kD, 192, 2, M, s));
+  AttnArgs a{m->qkv, m->seq_off, m->exp_tab, m->ctx, nseq, max_T, L.f[QR] + L.f[KR] + 3 - kFScore,
+             16 + L.f[VP] - L.f[CTX], L.bits[CTX]};
+  const int cb = L.bits[CTX] / 8;
+  HIPCHK(attention(a, cb, s));
+  if (tr && tr->attn_ctx) HIPCHK(hipMemcpyAsync(tr->attn_ctx, m->ctx, (size_t)M * kD * cb, hipMemcpyDeviceToDevice, s));
+  if ((rc = gemm_resid(L.o, m->ctx, cb, M, x, s))) return rc;
+  if (tr && tr->resid_mid) HIPCHK(hipMemcpyAsync(tr->resid_mid, x, (size_t)M * kD * 4, hipMemcpyDeviceToDevice, s));
+  const int h2b = L.bits[NORM2] / 8;
+  HIPCHK(rmsnorm(x, M, L.ln2, 21 + L.ln2_f - L.f[NORM2], L.bits[NORM2], m->h, h2b, s));
+  if (tr && tr->norm2_out) HIPCHK(hipMemcpyAsync(tr->norm2_out, m->h, (size_t)M * kD * h2b, hipMemcpyDeviceToDevice, s));
+  if ((rc = gemm_req(L.gu, m->h, h2b, M, m->gu, 16, s))) return rc;
+  if (tr && tr->gate_proj) HIPCHK(copy_cols(tr->gate_proj, kDFF, m->gu, 2 * kDFF, 0, kDFF, 2, M, s));
+  if (tr && tr->up_proj) HIPCHK(copy_cols(tr->up_proj, kDFF, m->gu, 2 * kDFF, kDFF, kDFF, 2, M, s));
+  const int gb = L.bits[GATED] / 8;
+  HIPCHK(silu_gate(m->gu, M, L.silu, L.f[SILU] + L.f[UP] - L.f_m, L.bits[GATED], m->gated, gb, s));
+  if (tr && tr->mlp_gated) HIPCHK(hipMemcpyAsync(tr->mlp_gated, m->gated, (size_t)M * kDFF * gb, hipMemcpyDeviceToDevice, s));
+  if ((rc = gemm_resid(L.down, m->gated, gb, M, x, s))) return rc;
+  return EII_OK;
+}
+
+int run_final(eii_model* m, const int32_t* x, int M, int32_t* logits, hipStream_t s) {
+  HIPCHK(rmsnorm(x, M, m->fg, 21 + m->fg_f - m->f_y, 16, m->h, 2, s));
+  GemmArgs g{m->h, m->head.W, M, kV, kD, m->head.wsum, m->head.mult, m->head.shift, logits, 32, m->flags};
+  HIPCHK(gemm(g, 2, EPI_LOGITS, s));
+  return EII_OK;
+}
+
+int forward_impl(eii_model* m, const int64_t* ids, const std::vector<int32_t>& lens, int32_t* emb_out,
+                 int32_t* res_out, int32_t* logits, hipStream_t s) {
+  size_t M = 0;
+  int max_T = 0;
+  for (int32_t t : lens) {
+    if (t <= 0) return fail(EII_E_ARG, "sequence length must be positive");
+    M += t;
+    max_T = std::max(max_T, (int)t);
+  }
+  if (M == 0) return EII_OK;
+  if (M > (size_t)INT32_MAX / kV) return fail(EII_E_ARG, "too many rows in one forward");
+  if (max_T > m->rope_rows)
+    return fail(EII_E_BOUND, "sequence of " + std::to_string(max_T) + " tokens exceeds the " +
+                                 std::to_string(m->rope_rows) + " RoPE rows loaded (eii_model_set_rope)");
+  if (max_T > 16384) return fail(EII_E_BOUND, "sequences longer than 16384 tokens are not supported");
+  HIPCHK(hipSetDevice(m->device));
+  int rc;
+  if ((rc = ensure_ws(m, M)) || (rc = set_batch(m, lens, s))) return rc;
+  const int Mi = (int)M;
+  HIPCHK(embed(ids, Mi, m->emb_q, m->emb_m, m->emb_sh, m->x, m->flags, s));
+  if (emb_out) HIPCHK(hipMemcpyAsync(emb_out, m->x, M * kD * 4, hipMemcpyDeviceToDevice, s));
+  for (int l = 0; l < kNL; ++l) {
+    if ((rc = run_block(m, l, m->x, Mi, (int)lens.size(), max_T, nullptr, s))) return rc;
+    if (res_out) HIPCHK(hipMemcpyAsync(res_out + (size_t)l * M * kD, m->x, M * kD * 4, hipMemcpyDeviceToDevice, s));
+  }
+  if (logits) return run_final(m, m->x, Mi, logits, s);
+  return EII_OK;
+}
+
+}  // namespace
+
+extern "C" int eii_forward(eii_model* m, const int64_t* ids, int B, int T, int32_t* emb_out, int32_t* res_out,
+                           int32_t* logits, void* stream) {
+  if (!m || !ids || B <= 0 || T <= 0) return fail(EII_E_ARG, "bad forward arguments");
+  std::vector<int32_t> lens(B, T);
+  return forward_impl(m, ids, lens, emb_out, res_out, logits, (hipStream_t)stream);
+}
+
+extern "C" int eii_forward_packed(eii_model* m, const int64_t* ids, const int32_t* seq_lens, int nseq,
+                                  int32_t* emb_out, int32_t* res_out, int32_t* logits, void* stream) {
+  if (!m || !ids || !seq_lens || nseq <= 0) return fail(EII_E_ARG, "bad forward arguments");
+  std::vector<int32_t> lens(seq_lens, seq_lens + nseq);
+  return forward_impl(m, ids, lens, emb_out, res_out, logits, (hipStream_t)stream);
+}
+
+extern "C" int eii_check(eii_model* m, void* stream) {
+  if (!m) return fail(EII_E_ARG, "null model");
+  HIPCHK(hipSetDevice(m->device));
+  HIPCHK(hipStreamSynchronize((hipStream_t)stream));
+  int f = 0;
+  HIPCHK(hipMemcpy(&f, m->flags, 4, hipMemcpyDeviceToHost));
+  HIPCHK(hipMemset(m->flags, 0, 4));
+  if (f & 2) return fail(EII_E_BOUND, "token id outside [0, 49152)");
+  if (f & 1) return fail(EII_E_BOUND, "a logit left the int32 range");
+  return EII_OK;
+}
+
+extern "C" int eii_block(eii_model* m, int layer, int32_t* x, int B, int T, const eii_trace* tr, void* stream) {
+  if (!m || !x || layer < 0 || layer >= kNL || B <= 0 || T <= 0) return fail(EII_E_ARG, "bad block arguments");
+  if (T > m->rope_rows) return fail(EII_E_BOUND, "T exceeds the RoPE rows loaded");
+  if (T > 16384) return fail(EII_E_BOUND, "sequences longer than 16384 tokens are not supported");
+  HIPCHK(hipSetDevice(m->device));
+  hipStream_t s = (hipStream_t)stream;
+  std::vector<int32_t> lens(B, T);
+  int rc;
+  if ((rc = ensure_ws(m, (size_t)B * T)) || (rc = set_batch(m, lens, s))) return rc;
+  return run_block(m, layer, x, B * T, B, T, tr, s);
+}
+
+extern "C" int eii_embed(eii_model* m, const int64_t* ids, int M, int32_t* x, void* stream) {
+  if (!m || !ids || !x || M <= 0) return fail(EII_E_ARG, "bad embed arguments");
+  HIPCHK(hipSetDevice(m->device));
+  HIPCHK(embed(ids, M, m->emb_q, m->emb_m, m->emb_sh, x, m->flags, (hipStream_t)stream));
+  return EII_OK;
+}
+
+extern "C" int eii_final(eii_model* m, const int32_t* x, int M, int32_t* logits, void* stream) {
+  if (!m || !x || !logits || M <= 0) return fail(EII_E_ARG, "bad final arguments");
+  HIPCHK(hipSetDevice(m->device));
+  int rc;
+  if ((rc = ensure_ws(m, M))) return rc;
+  return run_final(m, x, M, logits, (hipStream_t)stream);
+}
+
+// ------------------------------------------------------------------------------ operators
+extern "C" int eii_weight_colsum(const int8_t* W, int N, int K, int32_t* wsum, void* stream) {
+  if (!W || !wsum || N <= 0 || K <= 0) return fail(EII_E_ARG, "bad colsum arguments");
+  HIPCHK(weight_colsum(W, N, K, wsum, (hipStream_t)stream));
+  return EII_OK;
+}
+
+static int check_gemm_args(const void* A, int a_bits, const int8_t* W, int M, int N, int K) {
+  if (!A || !W || M <= 0 || N <= 0 || K <= 0) return fail(EII_E_ARG, "bad gemm arguments");
+  if (a_bits != 16 && a_bits != 32) return fail(EII_E_ARG, "a_bits must be 16 or 32");
+  if (K % 64) return fail(EII_E_ARG, "K must be a multiple of 64");
+  if (K > 65536) return fail(EII_E_BOUND, "K above 65536 could overflow a limb partial sum");
+  return EII_OK;
+}
+
+extern "C" int eii_gemm_i8_ws(const void* A, int a_bits, const int8_t* W, const int32_t* wsum, int M, int N, int K,
+                              int64_t* acc, void* stream) {
+  int rc;
+  if ((rc = check_gemm_args(A, a_bits, W, M, N, K))) return rc;
+  if (!wsum || !acc) return fail(EII_E_ARG, "null output");
+  GemmArgs g{A, W, M, N, K, wsum, nullptr, nullptr, acc, 64, nullptr};
+  HIPCHK(gemm(g, a_bits / 8, EPI_I64, (hipStream_t)stream));
+  return EII_OK;
+}
+
+extern "C" int eii_gemm_i8(const void* A, int a_bits, const int8_t* W, int M, int N, int K, int64_t* acc,
+                           void* stream) {
+  int rc;
+  if ((rc = check_gemm_args(A, a_bits, W, M, N, K))) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  int32_t* ws = nullptr;
+  HIPCHK(hipMallocAsync((void**)&ws, (size_t)N * 4, s));
+  rc = EII_OK;
+  hipError_t e = weight_colsum(W, N, K, ws, s);
+  if (e == hipSuccess) rc = eii_gemm_i8_ws(A, a_bits, W, ws, M, N, K, acc, stream);
+  else rc = fail(EII_E_DEVICE, hipGetErrorString(e));
+  (void)hipFreeAsync(ws, s);
+  return rc;
+}
+
+extern "C" int eii_linear(const void* A, int a_bits, const int8_t* W, const int32_t* wsum, const int32_t* mult,
+                          const int32_t* shift, int M, int N, int K, int out_bits, void* out, void* stream) {
+  int rc;
+  if ((rc = check_gemm_args(A, a_bits, W, M, N, K))) return rc;
+  if (!wsum || !mult || !shift || !out) return fail(EII_E_ARG, "null argument");
+  if (out_bits != 16 && out_bits != 32) return fail(EII_E_ARG, "out_bits must be 16 or 32");
+  GemmArgs g{A, W, M, N, K, wsum, mult, shift, out, out_bits, nullptr};
+  HIPCHK(gemm(g, a_bits / 8, out_bits == 16 ? EPI_REQ16 : EPI_REQ32, (hipStream_t)stream));
+  return EII_OK;
+}
+
+extern "C" int eii_rmsnorm(const int32_t* x, int M, const int32_t* gain, int f_gain, int f_out, int out_bits,
+                           void* out, void* stream) {
+  if (!x || !gain || !out || M <= 0) return fail(EII_E_ARG, "bad rmsnorm arguments");
+  if (out_bits != 16 && out_bits != 32) return fail(EII_E_ARG, "out_bits must be 16 or 32");
+  int rc;
+  if ((rc = check_scalar_shift(21 + f_gain - f_out, "norm"))) return rc;
+  HIPCHK(rmsnorm(x, M, gain, 21 + f_gain - f_out, out_bits, out, out_bits / 8, (hipStream_t)stream));
+  return EII_OK;
+}
+
+extern "C" int eii_attention(const int16_t* qkv, const int32_t* seq_off, int nseq, int max_T, const int32_t* exp_tab,
+                             int f_qr, int f_kr, int f_v, int f_c, int bits_c, void* ctx, void* stream) {
+  if (!qkv || !seq_off || !exp_tab || !ctx || nseq <= 0 || max_T <= 0) return fail(EII_E_ARG, "bad attention arguments");
+  if (bits_c != 16 && bits_c != 32) return fail(EII_E_ARG, "bits_c must be 16 or 32");
+  const int shift_s = f_qr + f_kr + 3 - kFScore;
+  if (shift_s < 1) return fail(EII_E_BOUND, "score shift < 1");
+  if (max_T > 16384) return fail(EII_E_BOUND, "sequences longer than 16384 tokens are not supported");
+  AttnArgs a{qkv, seq_off, exp_tab, ctx, nseq, max_T, shift_s, 16 + f_v - f_c, bits_c};
+  HIPCHK(attention(a, bits_c / 8, (hipStream_t)stream));
+  return EII_OK;
+}

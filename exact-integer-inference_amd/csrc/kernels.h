@@ -1,0 +1,60 @@
+// Launchers of the gfx950 kernels (kernels.hip).  All pointers are device pointers; every
+// launcher enqueues on the given stream and returns the launch status.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace eii {
+
+enum Epi : int {
+  EPI_I64 = 0,     // out int64 [M, N] = exact accumulator
+  EPI_REQ16 = 1,   // out int16 [M, N] = SAT(RS(acc * m[n], sh[n]), sat_bits)
+  EPI_REQ32 = 2,   // out int32 [M, N] = SAT(RS(acc * m[n], sh[n]), sat_bits)
+  EPI_RESID = 3,   // x int32 [M, N] = SAT32(x + RS(acc * m[n], sh[n]))
+  EPI_LOGITS = 4,  // out int32 [M, N] = RS(acc * m[n], sh[n]); *flag |= 1 if it leaves int32
+};
+
+struct GemmArgs {
+  const void* A;          // activations [M, K], int16 (a_bytes 2) or int32 (a_bytes 4)
+  const int8_t* W;        // weights [N, K], row = output channel
+  int M, N, K;            // K % 64 == 0
+  const int32_t* wsum;    // [N] sum_k W[n, k]
+  const int32_t* mult;    // [N] m (|m| <= 2^14)
+  const int32_t* shift;   // [N] requantization shift, 1..62
+  void* out;
+  int sat_bits;
+  int* flag;
+};
+
+hipError_t gemm(const GemmArgs& a, int a_bytes, int epi, hipStream_t s);
+hipError_t weight_colsum(const int8_t* W, int N, int K, int32_t* wsum, hipStream_t s);
+
+// x[m, c] = RS(emb_q[id, c] * emb_m[id], emb_sh[id]) (python/intref.py:163-166)
+hipError_t embed(const int64_t* ids, int M, const int8_t* emb_q, const int32_t* emb_m,
+                 const int32_t* emb_sh, int32_t* x, int* flag, hipStream_t s);
+
+// out = SAT(RS(3 * RS(x * U, 16) * gain, sh_out), bits_out), out int16 or int32 by out_bytes
+hipError_t rmsnorm(const int32_t* x, int M, const int32_t* gain, int sh_out, int bits_out,
+                   void* out, int out_bytes, hipStream_t s);
+
+// In-place rotate-half RoPE on the q (cols 0..575) and k (cols 576..767) parts of qkv [M, 960]
+hipError_t rope(int16_t* qkv, int M, const int32_t* pos, const int32_t* cosT, const int32_t* sinT,
+                int sh_q, int bits_q, int sh_k, int bits_k, hipStream_t s);
+
+// gated[m, j] = SAT(RS(silu[gu[m, j] + 32768] * gu[m, 1536 + j], sh), bits)
+hipError_t silu_gate(const int16_t* gu, int M, const int32_t* silu, int sh, int bits,
+                     void* gated, int out_bytes, hipStream_t s);
+
+struct AttnArgs {
+  const int16_t* qkv;      // [M, 960]: q rope | k rope | v
+  const int32_t* seq_off;  // [B + 1] row offsets of the sequences
+  const int32_t* exp_tab;  // [1537]
+  void* ctx;               // [M, 576], int16 or int32
+  int B, max_T;
+  int shift_s;             // f_qr + f_kr + 3 - 7
+  int sh_ctx;              // 16 + f_v - f_c
+  int bits_c;
+};
+hipError_t attention(const AttnArgs& a, int out_bytes, hipStream_t s);
+
+}  // namespace eii

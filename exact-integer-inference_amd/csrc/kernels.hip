@@ -1,0 +1,556 @@
+// gfx950 kernels of the exact integer forward (SmolLM2-135M shape).
+//
+// Integer projections run on v_mfma_i32_16x16x64_i8: activations wider than int8 are split
+// exactly into int8 limb planes while they are staged into LDS (eii_int.h), every limb plane
+// is multiplied with the same int8 weight tile, and the limb partial sums (each below 2^31)
+// are recombined in int64 in the epilogue, which also applies the reference's requantization.
+// The elementwise kernels are one pass over HBM each; attention computes QK and PV as
+// integer MFMA tiles with the reference's three-step exact softmax (row max, exp-table sum,
+// rounded Q0.16 division).
+#include "eii_int.h"
+#include "kernels.h"
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+namespace eii {
+
+namespace {
+
+constexpr int kBK = 64;          // K block: one MFMA K-step
+constexpr int kLdsRow = 80;      // LDS bytes per 64-byte row: 16-lane b128 reads hit 64 distinct banks
+
+__device__ __forceinline__ v4i mfma(v4i a, v4i b, v4i c) {
+  return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+// Limb planes of 4 int16 values packed in two dwords: (low bytes - 128, high bytes).
+__device__ __forceinline__ uint32_t lo_bytes16(uint32_t d0, uint32_t d1) {
+  return ((d0 & 0xFFu) | ((d0 >> 8) & 0xFF00u) | ((d1 << 16) & 0xFF0000u) | ((d1 << 8) & 0xFF000000u)) ^ 0x80808080u;
+}
+__device__ __forceinline__ uint32_t hi_bytes16(uint32_t d0, uint32_t d1) {
+  return ((d0 >> 8) & 0xFFu) | ((d0 >> 16) & 0xFF00u) | ((d1 << 8) & 0xFF0000u) | (d1 & 0xFF000000u);
+}
+// Byte plane i (0 = lowest) of 4 int32 values, biased by -128 unless it is the top byte.
+__device__ __forceinline__ uint32_t byte_plane32(uint4 d, int i) {
+  const int s = 8 * i;
+  uint32_t r = ((d.x >> s) & 0xFFu) | (((d.y >> s) & 0xFFu) << 8) | (((d.z >> s) & 0xFFu) << 16) |
+               (((d.w >> s) & 0xFFu) << 24);
+  return i == 3 ? r : (r ^ 0x80808080u);
+}
+
+// ------------------------------------------------------------------------------ GEMM
+template <int AW, int BM, int BN, int WM, int WN>
+struct GemmCfg {
+  static constexpr int kPlane = BM * kLdsRow;
+  static constexpr int kABytes = AW * kPlane;
+  static constexpr int kBBytes = BN * kLdsRow;
+  static constexpr int kStage = kABytes + kBBytes;
+  static constexpr int TM = WM / 16, TN = WN / 16;
+  static constexpr int kWavesN = BN / WN;
+  static constexpr int kAChunks = BM * 4 * AW / 256;   // 16-byte global loads per thread
+  static constexpr int kBChunks = BN * 4 / 256;
+  static_assert((BM / WM) * (BN / WN) == 4, "four waves per workgroup");
+  static_assert(kAChunks * 256 == BM * 4 * AW && kBChunks * 256 == BN * 4, "chunk split");
+};
+
+template <int AW, int BM, int BN, int WM, int WN, int EPI>
+__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
+  using C = GemmCfg<AW, BM, BN, WM, WN>;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * C::kStage];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / C::kWavesN, wn = wave % C::kWavesN;
+  const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
+  const int nk = g.K / kBK;
+  const uint8_t* Ab = (const uint8_t*)g.A;
+
+  uint4 areg[C::kAChunks], breg[C::kBChunks];
+
+  auto load = [&](int kb) {
+#pragma unroll
+    for (int i = 0; i < C::kAChunks; ++i) {
+      const int q = tid + 256 * i, row = q / (4 * AW), c = q % (4 * AW);
+      const int m = m0 + row;
+      areg[i] = m < g.M ? *(const uint4*)(Ab + ((size_t)m * g.K + (size_t)kb * kBK) * AW + c * 16)
+                        : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < C::kBChunks; ++i) {
+      const int q = tid + 256 * i, row = q / 4, c = q % 4;
+      const int n = n0 + row;
+      breg[i] = n < g.N ? *(const uint4*)(g.W + (size_t)n * g.K + (size_t)kb * kBK + c * 16)
+                        : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto store = [&](int st) {
+    uint8_t* base = smem + st * C::kStage;
+#pragma unroll
+    for (int i = 0; i < C::kAChunks; ++i) {
+      const int q = tid + 256 * i, row = q / (4 * AW), c = q % (4 * AW);
+      const uint4 d = areg[i];
+      if constexpr (AW == 2) {
+        uint8_t* p = base + row * kLdsRow + c * 8;       // 8 elements -> 8 bytes per plane
+        *(uint2*)(p) = make_uint2(lo_bytes16(d.x, d.y), lo_bytes16(d.z, d.w));
+        *(uint2*)(p + C::kPlane) = make_uint2(hi_bytes16(d.x, d.y), hi_bytes16(d.z, d.w));
+      } else {
+        uint8_t* p = base + row * kLdsRow + c * 4;       // 4 elements -> 4 bytes per plane
+#pragma unroll
+        for (int pl = 0; pl < 4; ++pl) *(uint32_t*)(p + pl * C::kPlane) = byte_plane32(d, pl);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < C::kBChunks; ++i) {
+      const int q = tid + 256 * i, row = q / 4, c = q % 4;
+      *(uint4*)(base + C::kABytes + row * kLdsRow + c * 16) = breg[i];
+    }
+  };
+
+  v4i acc[C::TM][C::TN][AW];
+#pragma unroll
+  for (int a = 0; a < C::TM; ++a)
+#pragma unroll
+    for (int b = 0; b < C::TN; ++b)
+#pragma unroll
+      for (int l = 0; l < AW; ++l) acc[a][b][l] = v4i{0, 0, 0, 0};
+
+  load(0);
+  store(0);
+  __syncthreads();
+  const int fr = lane & 15, fk = (lane >> 4) * 16;
+  for (int kb = 0; kb < nk; ++kb) {
+    const int cur = kb & 1;
+    if (kb + 1 < nk) load(kb + 1);
+    const uint8_t* base = smem + cur * C::kStage;
+    v4i bf[C::TN];
+#pragma unroll
+    for (int tn = 0; tn < C::TN; ++tn)
+      bf[tn] = *(const v4i*)(base + C::kABytes + (wn * WN + tn * 16 + fr) * kLdsRow + fk);
+#pragma unroll
+    for (int tm = 0; tm < C::TM; ++tm) {
+#pragma unroll
+      for (int l = 0; l < AW; ++l) {
+        const v4i af = *(const v4i*)(base + l * C::kPlane + (wm * WM + tm * 16 + fr) * kLdsRow + fk);
+#pragma unroll
+        for (int tn = 0; tn < C::TN; ++tn) acc[tm][tn][l] = mfma(af, bf[tn], acc[tm][tn][l]);
+      }
+    }
+    if (kb + 1 < nk) store(cur ^ 1);
+    __syncthreads();
+  }
+
+  // Epilogue: lane holds rows 4*(lane/16)+r, column lane%16 of each 16x16 tile.
+  const int64_t bias = limb_bias(AW);
+#pragma unroll
+  for (int tn = 0; tn < C::TN; ++tn) {
+    const int n = n0 + wn * WN + tn * 16 + fr;
+    if (n >= g.N) continue;
+    const int64_t cw = bias * (int64_t)g.wsum[n];
+    int32_t mu = 0, sh = 1;
+    if constexpr (EPI != EPI_I64) { mu = g.mult[n]; sh = g.shift[n]; }
+#pragma unroll
+    for (int tm = 0; tm < C::TM; ++tm) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = m0 + wm * WM + tm * 16 + (lane >> 4) * 4 + r;
+        if (m >= g.M) continue;
+        int64_t a = cw;
+#pragma unroll
+        for (int l = 0; l < AW; ++l) a += (int64_t)acc[tm][tn][l][r] * ((int64_t)1 << (8 * l));
+        const size_t o = (size_t)m * g.N + n;
+        if constexpr (EPI == EPI_I64) {
+          ((int64_t*)g.out)[o] = a;
+        } else {
+          const int64_t v = rs(a * mu, sh);
+          if constexpr (EPI == EPI_REQ16) {
+            ((int16_t*)g.out)[o] = (int16_t)sat(v, g.sat_bits);
+          } else if constexpr (EPI == EPI_REQ32) {
+            ((int32_t*)g.out)[o] = (int32_t)sat(v, g.sat_bits);
+          } else if constexpr (EPI == EPI_RESID) {
+            int32_t* x = (int32_t*)g.out;
+            x[o] = (int32_t)clamp_bits32((int64_t)x[o] + v);
+          } else {
+            if (v != (int64_t)(int32_t)v) atomicOr(g.flag, 1);
+            ((int32_t*)g.out)[o] = (int32_t)v;
+          }
+        }
+      }
+    }
+  }
+}
+
+template <int AW, int EPI>
+hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
+  constexpr int BM = AW == 2 ? 128 : 64, BN = 128, WM = AW == 2 ? 64 : 32, WN = 64;
+  dim3 grid((a.N + BN - 1) / BN, (a.M + BM - 1) / BM);
+  hipLaunchKernelGGL((gemm_kernel<AW, BM, BN, WM, WN, EPI>), grid, dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+__global__ __launch_bounds__(256) void colsum_kernel(const int8_t* W, int N, int K, int32_t* wsum) {
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (n >= N) return;
+  int32_t s = 0;
+  for (int k = lane; k < K; k += 64) s += W[(size_t)n * K + k];
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+  if (lane == 0) wsum[n] = s;
+}
+
+// ------------------------------------------------------------------------------ embed
+__global__ __launch_bounds__(256) void embed_kernel(const int64_t* ids, int M, const int8_t* emb_q,
+                                                    const int32_t* emb_m, const int32_t* emb_sh,
+                                                    int32_t* x, int* flag) {
+  const size_t t = (size_t)blockIdx.x * 256 + threadIdx.x;     // 4 elements per thread
+  if (t >= (size_t)M * (kD / 4)) return;
+  const int row = (int)(t / (kD / 4)), c4 = (int)(t % (kD / 4));
+  int64_t id = ids[row];
+  if (id < 0 || id >= kV) { atomicOr(flag, 2); id = 0; }
+  const uint32_t q4 = *(const uint32_t*)(emb_q + (size_t)id * kD + 4 * c4);
+  const int64_t mu = emb_m[id];
+  const int sh = emb_sh[id];
+  int4 o;
+  o.x = (int32_t)rs((int64_t)(int8_t)(q4 & 0xFF) * mu, sh);
+  o.y = (int32_t)rs((int64_t)(int8_t)((q4 >> 8) & 0xFF) * mu, sh);
+  o.z = (int32_t)rs((int64_t)(int8_t)((q4 >> 16) & 0xFF) * mu, sh);
+  o.w = (int32_t)rs((int64_t)(int8_t)(q4 >> 24) * mu, sh);
+  *(int4*)(x + (size_t)row * kD + 4 * c4) = o;
+}
+
+// ------------------------------------------------------------------------------ rmsnorm
+// One wave per row; lane j holds elements j, j+64, ..., j+512.
+template <int OB>
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const int32_t* x, int M, const int32_t* gain,
+                                                      int sh_out, int bits_out, void* out) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (row >= M) return;
+  const int32_t* xr = x + (size_t)row * kD;
+  int32_t v[9];
+  int64_t A = 0, B = 0, Cs = 0;
+#pragma unroll
+  for (int j = 0; j < 9; ++j) {
+    v[j] = xr[lane + 64 * j];
+    const int64_t hi = v[j] >> 16, lo = v[j] & 0xFFFF;
+    A += hi * hi; B += hi * lo; Cs += lo * lo;
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    A += __shfl_xor(A, o); B += __shfl_xor(B, o); Cs += __shfl_xor(Cs, o);
+  }
+  const int64_t U = norm_U(norm_total(A, B, Cs));
+#pragma unroll
+  for (int j = 0; j < 9; ++j) {
+    const int c = lane + 64 * j;
+    const int64_t z = rs((int64_t)v[j] * U, 16);
+    const int64_t o = sat(rs(z * gain[c] * 3, sh_out), bits_out);
+    if constexpr (OB == 2) ((int16_t*)out)[(size_t)row * kD + c] = (int16_t)o;
+    else ((int32_t*)out)[(size_t)row * kD + c] = (int32_t)o;
+  }
+}
+
+// ------------------------------------------------------------------------------ rope
+__global__ __launch_bounds__(256) void rope_kernel(int16_t* qkv, int M, const int32_t* pos,
+                                                   const int32_t* cosT, const int32_t* sinT,
+                                                   int sh_q, int bits_q, int sh_k, int bits_k) {
+  const size_t t = (size_t)blockIdx.x * 256 + threadIdx.x;     // one (d, d+32) pair
+  if (t >= (size_t)M * 384) return;
+  const int row = (int)(t / 384), p = (int)(t % 384), h = p >> 5, d = p & 31;
+  const int col = h * 64 + d;                                    // heads 0..8 q, 9..11 k
+  const int sh = h < 9 ? sh_q : sh_k, bits = h < 9 ? bits_q : bits_k;
+  int16_t* r = qkv + (size_t)row * kQKVN + col;
+  const int64_t a1 = r[0], a2 = r[32];
+  const int ps = pos[row];
+  const int64_t c = cosT[ps * 32 + d], s = sinT[ps * 32 + d];
+  r[0] = (int16_t)sat(rs(a1 * c - a2 * s, sh), bits);
+  r[32] = (int16_t)sat(rs(a2 * c + a1 * s, sh), bits);
+}
+
+// ------------------------------------------------------------------------------ silu gate
+template <int OB>
+__global__ __launch_bounds__(256) void silu_kernel(const int16_t* gu, int M, const int32_t* silu,
+                                                   int sh, int bits, void* gated) {
+  const size_t t = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= (size_t)M * kDFF) return;
+  const size_t row = t / kDFF, j = t % kDFF;
+  const int g = gu[row * (2 * kDFF) + j];
+  const int64_t u = gu[row * (2 * kDFF) + kDFF + j];
+  const int64_t o = sat(rs((int64_t)silu[g + 32768] * u, sh), bits);
+  if constexpr (OB == 2) ((int16_t*)gated)[t] = (int16_t)o;
+  else ((int32_t*)gated)[t] = (int32_t)o;
+}
+
+// ------------------------------------------------------------------------------ attention
+// Workgroup = (64-query block, q head, sequence); wave w owns queries q0+16w .. q0+16w+15.
+// Scores are computed transposed, S^T[key][query] = K . Q^T, so a lane holds one query
+// column and the probabilities P[key][query] land directly in the B-operand layout of the
+// PV product ctx^T[d][query] = V^T . P (the K-slot order of an MFMA is free as long as the A
+// and B operands use the same one).  Limb algebra, with x^ = x - 128 split as 256*H + L':
+//   sum_d q k = 65536 sum QH KH + 256 (sum QH KL' + sum QL' KH) + sum QL' KL'
+//               + 128 (sum_d q^ + sum_d k^) + 64 * 128^2
+//   sum_j P v = 2^24 sum P2 VH + 2^16 (sum P1' VH + sum P2 VL') + 2^8 (sum P0' VH + sum P1' VL')
+//               + sum P0' VL' + 32896 sum_j v^ + 128 sum_j P
+// with P = 65536 P2 + 256 (P1' + 128) + (P0' + 128).
+template <int OB>
+__global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t kpl[2][64 * kLdsRow];   // K planes, row = key
+  __shared__ __attribute__((aligned(16))) uint8_t vpl[2][64 * kLdsRow];   // V^T planes, row = d
+  __shared__ int32_t sk[64];
+  __shared__ int64_t cv[64];
+  __shared__ int32_t etab[kDMax + 1];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, gq = lane >> 4, c16 = lane & 15;
+  const int b = blockIdx.z, hh = blockIdx.y, qb = gridDim.x - 1 - blockIdx.x;
+  const int s0 = a.seq_off[b], T = a.seq_off[b + 1] - s0, q0 = qb * 64;
+  if (q0 >= T) return;
+  const int kvg = hh / 3;
+  const int qi = q0 + 16 * w + c16;
+
+  for (int i = tid; i <= kDMax; i += 256) etab[i] = a.exp_tab[i];
+  if (tid < 64) cv[tid] = 0;
+
+  // Q B-fragment: query qi, d = 16*gq .. 16*gq+15
+  v4i QH, QL;
+  int32_t sq;
+  {
+    uint4 d0 = make_uint4(0, 0, 0, 0), d1 = d0;
+    if (qi < T) {
+      const int16_t* qp = a.qkv + (size_t)(s0 + qi) * kQKVN + hh * 64 + 16 * gq;
+      d0 = *(const uint4*)qp;
+      d1 = *(const uint4*)(qp + 8);
+    }
+    QL = v4i{(int)lo_bytes16(d0.x, d0.y), (int)lo_bytes16(d0.z, d0.w), (int)lo_bytes16(d1.x, d1.y),
+             (int)lo_bytes16(d1.z, d1.w)};
+    QH = v4i{(int)hi_bytes16(d0.x, d0.y), (int)hi_bytes16(d0.z, d0.w), (int)hi_bytes16(d1.x, d1.y),
+             (int)hi_bytes16(d1.z, d1.w)};
+    const uint32_t dw[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+    sq = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) sq += (int32_t)(int16_t)(dw[i] & 0xFFFF) + (int32_t)(int16_t)(dw[i] >> 16);
+    sq += __shfl_xor(sq, 16);
+    sq += __shfl_xor(sq, 32);
+    sq -= 64 * 128;
+  }
+
+  const int nkb = min(qb + 1, (T + 63) / 64);
+  int32_t rowmax = -(1 << 20);
+  int64_t Z = 0, SP = 0;
+  double rZ = 0.0;
+  v4i C24[4], C16[4], C8[4], C0[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) C24[i] = C16[i] = C8[i] = C0[i] = v4i{0, 0, 0, 0};
+
+  for (int pass = 0; pass < 3; ++pass) {
+    for (int kb = 0; kb < nkb; ++kb) {
+      __syncthreads();
+      // stage K (and in the last pass V^T) for keys kb*64 .. kb*64+63
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int q = tid + 256 * i, jj = q >> 3, c = q & 7, j = kb * 64 + jj;
+        uint4 d = make_uint4(0, 0, 0, 0);
+        if (j < T) d = *(const uint4*)(a.qkv + (size_t)(s0 + j) * kQKVN + kD + kvg * 64 + 8 * c);
+        *(uint2*)(&kpl[0][jj * kLdsRow + 8 * c]) = make_uint2(lo_bytes16(d.x, d.y), lo_bytes16(d.z, d.w));
+        *(uint2*)(&kpl[1][jj * kLdsRow + 8 * c]) = make_uint2(hi_bytes16(d.x, d.y), hi_bytes16(d.z, d.w));
+        int32_t s = 0;
+        const uint32_t dw[4] = {d.x, d.y, d.z, d.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) s += (int32_t)(int16_t)(dw[e] & 0xFFFF) + (int32_t)(int16_t)(dw[e] >> 16);
+        s += __shfl_xor(s, 1);
+        s += __shfl_xor(s, 2);
+        s += __shfl_xor(s, 4);
+        if (c == 0) sk[jj] = s - 64 * 128;
+        if (pass == 2) {
+          uint4 dv = make_uint4(0, 0, 0, 0);
+          if (j < T) dv = *(const uint4*)(a.qkv + (size_t)(s0 + j) * kQKVN + kD + 192 + kvg * 64 + 8 * c);
+          const uint32_t vw[4] = {dv.x, dv.y, dv.z, dv.w};
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const uint32_t v16 = (vw[e >> 1] >> (16 * (e & 1))) & 0xFFFF;
+            const int dd = 8 * c + e;
+            vpl[0][dd * kLdsRow + jj] = (uint8_t)((v16 & 0xFF) ^ 0x80);
+            vpl[1][dd * kLdsRow + jj] = (uint8_t)(v16 >> 8);
+          }
+        }
+      }
+      __syncthreads();
+      if (pass == 2 && tid < 64) {
+        int32_t s = 0;
+        for (int jj = 0; jj < 64; ++jj)
+          s += (int32_t)(int8_t)vpl[1][tid * kLdsRow + jj] * 256 + (int32_t)(int8_t)vpl[0][tid * kLdsRow + jj];
+        cv[tid] += s;
+      }
+
+      // scores for keys kb*64 + kt*16 + 4*gq + r, query qi
+      int32_t sc[4][4];
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        const v4i KH = *(const v4i*)(&kpl[1][(kt * 16 + c16) * kLdsRow + 16 * gq]);
+        const v4i KL = *(const v4i*)(&kpl[0][(kt * 16 + c16) * kLdsRow + 16 * gq]);
+        const v4i z = v4i{0, 0, 0, 0};
+        const v4i a16 = mfma(KH, QH, z);
+        v4i a8 = mfma(KH, QL, z);
+        a8 = mfma(KL, QH, a8);
+        const v4i a0 = mfma(KL, QL, z);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int jj = kt * 16 + 4 * gq + r;
+          const int64_t acc = (int64_t)a16[r] * 65536 + (int64_t)a8[r] * 256 + a0[r] +
+                              128 * (int64_t)(sk[jj] + sq) + (1 << 20);
+          sc[kt][r] = (int32_t)clamp_bits16(rs(acc, a.shift_s));
+        }
+      }
+
+      if (pass == 0) {
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int j = kb * 64 + kt * 16 + 4 * gq + r;
+            if (j <= qi && sc[kt][r] > rowmax) rowmax = sc[kt][r];
+          }
+      } else {
+        uint32_t p2w[4], p1w[4], p0w[4];
+        bool any2 = false;
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) {
+          p2w[kt] = p1w[kt] = p0w[kt] = 0;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int j = kb * 64 + kt * 16 + 4 * gq + r;
+            const int dd = rowmax - sc[kt][r];
+            const int64_t e = (j <= qi && dd <= kDMax) ? etab[dd] : 0;
+            if (pass == 1) {
+              Z += e;
+            } else {
+              const int64_t P = attn_prob(e, Z, rZ);
+              SP += P;
+              const uint32_t p = (uint32_t)P;
+              p2w[kt] |= (p >> 16) << (8 * r);
+              p1w[kt] |= (((p >> 8) & 0xFFu) ^ 0x80u) << (8 * r);
+              p0w[kt] |= ((p & 0xFFu) ^ 0x80u) << (8 * r);
+              any2 |= (p >> 16) != 0;
+            }
+          }
+        }
+        if (pass == 2) {
+          const v4i P2 = v4i{(int)p2w[0], (int)p2w[1], (int)p2w[2], (int)p2w[3]};
+          const v4i P1 = v4i{(int)p1w[0], (int)p1w[1], (int)p1w[2], (int)p1w[3]};
+          const v4i P0 = v4i{(int)p0w[0], (int)p0w[1], (int)p0w[2], (int)p0w[3]};
+          const bool wave2 = __any(any2);
+#pragma unroll
+          for (int dt = 0; dt < 4; ++dt) {
+            const int dd = dt * 16 + c16;
+            v4i VH, VL;
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt) {
+              VH[kt] = *(const int*)(&vpl[1][dd * kLdsRow + 16 * kt + 4 * gq]);
+              VL[kt] = *(const int*)(&vpl[0][dd * kLdsRow + 16 * kt + 4 * gq]);
+            }
+            C16[dt] = mfma(VH, P1, C16[dt]);
+            C8[dt] = mfma(VH, P0, C8[dt]);
+            C8[dt] = mfma(VL, P1, C8[dt]);
+            C0[dt] = mfma(VL, P0, C0[dt]);
+            if (wave2) {
+              C24[dt] = mfma(VH, P2, C24[dt]);
+              C16[dt] = mfma(VL, P2, C16[dt]);
+            }
+          }
+        }
+      }
+    }
+    if (pass == 0) {
+      rowmax = max(rowmax, __shfl_xor(rowmax, 16));
+      rowmax = max(rowmax, __shfl_xor(rowmax, 32));
+    } else if (pass == 1) {
+      Z += __shfl_xor(Z, 16);
+      Z += __shfl_xor(Z, 32);
+      rZ = 1.0 / (double)Z;
+    } else {
+      SP += __shfl_xor(SP, 16);
+      SP += __shfl_xor(SP, 32);
+    }
+  }
+  __syncthreads();
+  if (qi >= T) return;
+  const size_t orow = (size_t)(s0 + qi) * kD + hh * 64;
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int d = dt * 16 + 4 * gq + r;
+      const int64_t acc = (int64_t)C24[dt][r] * (1LL << 24) + (int64_t)C16[dt][r] * 65536 +
+                          (int64_t)C8[dt][r] * 256 + C0[dt][r] + 32896 * cv[d] + 128 * SP;
+      const int64_t o = sat(rs(acc, a.sh_ctx), a.bits_c);
+      if constexpr (OB == 2) ((int16_t*)a.ctx)[orow + d] = (int16_t)o;
+      else ((int32_t*)a.ctx)[orow + d] = (int32_t)o;
+    }
+  }
+}
+
+inline unsigned blocks_for(size_t n) { return (unsigned)((n + 255) / 256); }
+
+}  // namespace
+
+hipError_t gemm(const GemmArgs& a, int a_bytes, int epi, hipStream_t s) {
+  if (a.K % kBK != 0 || a.M <= 0 || a.N <= 0) return hipErrorInvalidValue;
+  if (a_bytes == 2) {
+    switch (epi) {
+      case EPI_I64: return launch_gemm<2, EPI_I64>(a, s);
+      case EPI_REQ16: return launch_gemm<2, EPI_REQ16>(a, s);
+      case EPI_REQ32: return launch_gemm<2, EPI_REQ32>(a, s);
+      case EPI_RESID: return launch_gemm<2, EPI_RESID>(a, s);
+      case EPI_LOGITS: return launch_gemm<2, EPI_LOGITS>(a, s);
+    }
+  } else if (a_bytes == 4) {
+    switch (epi) {
+      case EPI_I64: return launch_gemm<4, EPI_I64>(a, s);
+      case EPI_REQ16: return launch_gemm<4, EPI_REQ16>(a, s);
+      case EPI_REQ32: return launch_gemm<4, EPI_REQ32>(a, s);
+      case EPI_RESID: return launch_gemm<4, EPI_RESID>(a, s);
+      case EPI_LOGITS: return launch_gemm<4, EPI_LOGITS>(a, s);
+    }
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t weight_colsum(const int8_t* W, int N, int K, int32_t* wsum, hipStream_t s) {
+  hipLaunchKernelGGL(colsum_kernel, dim3((N + 3) / 4), dim3(256), 0, s, W, N, K, wsum);
+  return hipGetLastError();
+}
+
+hipError_t embed(const int64_t* ids, int M, const int8_t* emb_q, const int32_t* emb_m,
+                 const int32_t* emb_sh, int32_t* x, int* flag, hipStream_t s) {
+  hipLaunchKernelGGL(embed_kernel, dim3(blocks_for((size_t)M * (kD / 4))), dim3(256), 0, s, ids, M,
+                     emb_q, emb_m, emb_sh, x, flag);
+  return hipGetLastError();
+}
+
+hipError_t rmsnorm(const int32_t* x, int M, const int32_t* gain, int sh_out, int bits_out, void* out,
+                   int out_bytes, hipStream_t s) {
+  dim3 grid((M + 3) / 4);
+  if (out_bytes == 2) hipLaunchKernelGGL(rmsnorm_kernel<2>, grid, dim3(256), 0, s, x, M, gain, sh_out, bits_out, out);
+  else hipLaunchKernelGGL(rmsnorm_kernel<4>, grid, dim3(256), 0, s, x, M, gain, sh_out, bits_out, out);
+  return hipGetLastError();
+}
+
+hipError_t rope(int16_t* qkv, int M, const int32_t* pos, const int32_t* cosT, const int32_t* sinT, int sh_q,
+                int bits_q, int sh_k, int bits_k, hipStream_t s) {
+  hipLaunchKernelGGL(rope_kernel, dim3(blocks_for((size_t)M * 384)), dim3(256), 0, s, qkv, M, pos, cosT, sinT,
+                     sh_q, bits_q, sh_k, bits_k);
+  return hipGetLastError();
+}
+
+hipError_t silu_gate(const int16_t* gu, int M, const int32_t* silu, int sh, int bits, void* gated, int out_bytes,
+                     hipStream_t s) {
+  dim3 grid(blocks_for((size_t)M * kDFF));
+  if (out_bytes == 2) hipLaunchKernelGGL(silu_kernel<2>, grid, dim3(256), 0, s, gu, M, silu, sh, bits, gated);
+  else hipLaunchKernelGGL(silu_kernel<4>, grid, dim3(256), 0, s, gu, M, silu, sh, bits, gated);
+  return hipGetLastError();
+}
+
+hipError_t attention(const AttnArgs& a, int out_bytes, hipStream_t s) {
+  if (a.B <= 0 || a.max_T <= 0) return hipSuccess;
+  dim3 grid((a.max_T + 63) / 64, kNH, a.B);
+  if (out_bytes == 2) hipLaunchKernelGGL(attn_kernel<2>, grid, dim3(256), 0, s, a);
+  else hipLaunchKernelGGL(attn_kernel<4>, grid, dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+}  // namespace eii

@@ -1,0 +1,163 @@
+"""GPU engine: a loaded model.bin on one MI355X, driven through libeii's C ABI.
+
+torch provides device memory and the current HIP stream; all arithmetic runs in the
+library's gfx950 kernels.  Tensors passed in must live on the engine's device.
+"""
+import ctypes as C
+
+import numpy as np
+import torch
+
+from . import lib as L
+from . import modelbin as mb
+from .tables import rope_tables
+
+V, D, NL = mb.V, mb.D, mb.NL
+
+
+def _ptr(t):
+    return C.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _stream():
+    return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+class Engine:
+    """A model.bin resident on `device` (python/intref.py Model, batched and on the GPU)."""
+
+    def __init__(self, model_bin, device=0, rope_rows=None):
+        if not torch.cuda.is_available():
+            raise L.EIIError(L.EII_E_DEVICE, "no GPU visible to torch")
+        self.lib = L.load()
+        self.device = torch.device("cuda", device)
+        torch.cuda.set_device(self.device)
+        h = C.c_void_p()
+        L.check(self.lib.eii_model_load(str(model_bin).encode(), device, C.byref(h)))
+        self.h = h
+        self.path = str(model_bin)
+        if rope_rows and rope_rows > mb.ROPE_POS:
+            self.set_rope(rope_rows)
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.lib.eii_model_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # ------------------------------------------------------------------ model data
+    def set_rope(self, rows):
+        """Load RoPE tables for positions 0..rows-1 (python/intref.py:96-108)."""
+        Ct, St = rope_tables(rows)
+        Ct = np.ascontiguousarray(Ct, dtype=np.int64)
+        St = np.ascontiguousarray(St, dtype=np.int64)
+        L.check(self.lib.eii_model_set_rope(self.h, Ct.ctypes.data_as(L.i64p), St.ctypes.data_as(L.i64p), rows))
+
+    @property
+    def rope_rows(self):
+        return self.lib.eii_model_rope_rows(self.h)
+
+    def formats(self, layer):
+        fm = np.zeros(24, dtype=np.int64)
+        fy = np.zeros(1, dtype=np.int64)
+        L.check(self.lib.eii_model_formats(self.h, layer, fm.ctypes.data_as(L.i64p), fy.ctypes.data_as(L.i64p)))
+        return fm, int(fy[0])
+
+    def ensure_rope(self, T):
+        if T > self.rope_rows:
+            self.set_rope(max(T, 2 * self.rope_rows))
+
+    # ------------------------------------------------------------------ forward
+    def forward(self, ids, embed=False, resid=False, logits=True, check=True):
+        """ids int64 [B, T] (torch on the device, or numpy) -> dict of device tensors:
+        'embed' int32 [B, T, 576], 'resid' int32 [30, B, T, 576], 'logits' int32 [B, T, 49152]."""
+        ids = self._ids(ids)
+        B, T = ids.shape
+        self.ensure_rope(T)
+        out = self._alloc(B * T, embed, resid, logits)
+        L.check(self.lib.eii_forward(self.h, _ptr(ids), B, T, _ptr(out.get("embed")), _ptr(out.get("resid")),
+                                     _ptr(out.get("logits")), _stream()))
+        if check:
+            self.check()
+        return self._shape(out, (B, T))
+
+    def forward_packed(self, ids, seq_lens, embed=False, resid=False, logits=True, check=True):
+        """Ragged batch: ids int64 [sum(seq_lens)] packed sequence after sequence."""
+        ids = self._ids(ids).reshape(-1)
+        lens = np.ascontiguousarray(seq_lens, dtype=np.int32)
+        assert int(lens.sum()) == ids.numel()
+        self.ensure_rope(int(lens.max()))
+        out = self._alloc(ids.numel(), embed, resid, logits)
+        L.check(self.lib.eii_forward_packed(self.h, _ptr(ids), lens.ctypes.data_as(L.i32p), len(lens),
+                                            _ptr(out.get("embed")), _ptr(out.get("resid")),
+                                            _ptr(out.get("logits")), _stream()))
+        if check:
+            self.check()
+        return out
+
+    def check(self):
+        L.check(self.lib.eii_check(self.h, _stream()))
+
+    def block(self, layer, x, B, T, trace=False):
+        """x int32 [B*T, 576] device tensor, updated in place; returns the trace dict if asked."""
+        self.ensure_rope(T)
+        tr = None
+        bufs = {}
+        if trace:
+            fm, _ = self.formats(layer)
+            bits = {s: int(fm[2 * i]) for i, s in enumerate(mb.SITES)}
+            width = {"norm1_out": D, "q_proj": D, "k_proj": 192, "v_proj": 192, "q_rope": D, "k_rope": 192,
+                     "attn_ctx": D, "norm2_out": D, "gate_proj": 1536, "up_proj": 1536, "mlp_gated": 1536}
+            for s, w in width.items():
+                dt = torch.int16 if bits[s] == 16 else torch.int32
+                bufs[s] = torch.empty((B * T, w), dtype=dt, device=self.device)
+            bufs["resid_mid"] = torch.empty((B * T, D), dtype=torch.int32, device=self.device)
+            tr = L.eii_trace(**{k: v.data_ptr() for k, v in bufs.items()})
+        L.check(self.lib.eii_block(self.h, layer, _ptr(x), B, T, C.byref(tr) if tr is not None else None, _stream()))
+        return bufs
+
+    def embed(self, ids):
+        ids = self._ids(ids).reshape(-1)
+        x = torch.empty((ids.numel(), D), dtype=torch.int32, device=self.device)
+        L.check(self.lib.eii_embed(self.h, _ptr(ids), ids.numel(), _ptr(x), _stream()))
+        self.check()
+        return x
+
+    def final(self, x):
+        M = x.shape[0]
+        lg = torch.empty((M, V), dtype=torch.int32, device=self.device)
+        L.check(self.lib.eii_final(self.h, _ptr(x), M, _ptr(lg), _stream()))
+        self.check()
+        return lg
+
+    # ------------------------------------------------------------------ helpers
+    def _ids(self, ids):
+        if isinstance(ids, np.ndarray):
+            ids = torch.from_numpy(np.ascontiguousarray(ids, dtype=np.int64))
+        ids = ids.to(device=self.device, dtype=torch.int64).contiguous()
+        if ids.dim() == 1:
+            ids = ids[None, :]
+        return ids
+
+    def _alloc(self, M, embed, resid, logits):
+        out = {}
+        if embed:
+            out["embed"] = torch.empty((M, D), dtype=torch.int32, device=self.device)
+        if resid:
+            out["resid"] = torch.empty((NL, M, D), dtype=torch.int32, device=self.device)
+        if logits:
+            out["logits"] = torch.empty((M, V), dtype=torch.int32, device=self.device)
+        return out
+
+    @staticmethod
+    def _shape(out, bt):
+        B, T = bt
+        r = {}
+        for k, v in out.items():
+            r[k] = v.view(NL, B, T, -1) if k == "resid" else v.view(B, T, -1)
+        return r

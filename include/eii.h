@@ -1,0 +1,120 @@
+/* libeii: exact integer forward of the SmolLM2-135M-shaped model on one MI355X (gfx950).
+ *
+ * C ABI for the hot path of the reference's integer engine.  All pointers named *_dev are
+ * device pointers (e.g. a torch tensor's data_ptr()); `stream` is a hipStream_t or NULL for
+ * the default stream.  Every call enqueues its work on the stream and returns without
+ * waiting, except where stated.  The library owns the model's device arrays and its
+ * activation workspace; the caller owns every input and output buffer.
+ *
+ * Status codes mirror the exit codes of the reference checkers (c/intref.c:63,67,215,
+ * cuda/intref.cu:22,263-273): 0 ok, 2 file/format error, 3 device error, 4 a bound the
+ * semantics require is violated (shift < 1, table too short, value out of range),
+ * 5 invalid argument.  eii_last_error() describes the last failure of the calling thread.
+ */
+#ifndef EII_H
+#define EII_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define EII_OK 0
+#define EII_E_IO 2
+#define EII_E_DEVICE 3
+#define EII_E_BOUND 4
+#define EII_E_ARG 5
+
+typedef struct eii_model eii_model;
+
+/* Optional per-site dumps of one block (python/intref.py:198-285 `trace`).  Each non-NULL
+ * pointer receives [rows, width] values in the site's declared width: int16 for 16-bit sites,
+ * int32 for 32-bit sites (widths: q/norm/ctx 576, k/v 192, gate/up/gated 1536). */
+typedef struct {
+  void* norm1_out; void* q_proj; void* k_proj; void* v_proj; void* q_rope; void* k_rope;
+  void* attn_ctx; int32_t* resid_mid; void* norm2_out; void* gate_proj; void* up_proj;
+  void* mlp_gated;
+} eii_trace;
+
+const char* eii_last_error(void);
+
+/* Load a model.bin (python/export_vectors.py:24-45; read order of c/intref.c:70-91 and
+ * cuda/intref.cu:184-206) onto `device`.  int64 fields are narrowed to the widths the
+ * semantics allow and every narrowing is checked; per-row requantization shifts must be
+ * >= 1 as python/intref.py:49 asserts. */
+int eii_model_load(const char* model_bin_path, int device, eii_model** out);
+void eii_model_free(eii_model* m);
+
+/* Replace the RoPE tables by host arrays cos/sin int64 [rows, 32] (Q30), e.g. rows beyond
+ * the 512 model.bin holds (python/intref.py:96-108 is defined for any T). */
+int eii_model_set_rope(eii_model* m, const int64_t* cos_host, const int64_t* sin_host, int rows);
+int eii_model_rope_rows(const eii_model* m);
+
+/* (bits, f) of the 12 sites of layer l in fm order, into fm24[24]; f_y into *f_y. */
+int eii_model_formats(const eii_model* m, int layer, int64_t* fm24, int64_t* f_y);
+
+/* Batched forward (python/intref.py:288-301 for B independent sequences of T tokens).
+ * ids_dev int64 [B*T].  Outputs, each optional (NULL = not written):
+ *   embed_out_dev int32 [B*T, 576]; resid_out_dev int32 [30, B*T, 576] (after each block);
+ *   logits_dev int32 [B*T, 49152] (f = 16; exact when |logit| < 2^31, which
+ *   python/export_vectors.py:58 asserts; eii_check reports a logit outside int32). */
+int eii_forward(eii_model* m, const int64_t* ids_dev, int B, int T, int32_t* embed_out_dev,
+                int32_t* resid_out_dev, int32_t* logits_dev, void* stream);
+
+/* Ragged batch: seq_lens_host[nseq] tokens per sequence, ids packed sequence after sequence. */
+int eii_forward_packed(eii_model* m, const int64_t* ids_dev, const int32_t* seq_lens_host, int nseq,
+                       int32_t* embed_out_dev, int32_t* resid_out_dev, int32_t* logits_dev,
+                       void* stream);
+
+/* Waits for `stream`, then reports data-dependent violations seen since the last check:
+ * a token id outside [0, 49152) or a logit outside int32 (status 4). */
+int eii_check(eii_model* m, void* stream);
+
+/* One decoder block in place on x_dev int32 [B*T, 576] (python/intref.py:192-286),
+ * optional per-site dumps. */
+int eii_block(eii_model* m, int layer, int32_t* x_dev, int B, int T, const eii_trace* trace,
+              void* stream);
+
+/* Embedding lookup (python/intref.py:163-166): ids_dev int64 [M] -> x_dev int32 [M, 576]. */
+int eii_embed(eii_model* m, const int64_t* ids_dev, int M, int32_t* x_dev, void* stream);
+
+/* Final RMSNorm and tied head (python/intref.py:296-301): x_dev int32 [M, 576] ->
+ * logits_dev int32 [M, 49152]. */
+int eii_final(eii_model* m, const int32_t* x_dev, int M, int32_t* logits_dev, void* stream);
+
+/* ---- operator level (python/intref.py functions) ---- */
+
+/* Row sums of int8 weights W_dev [N, K] into wsum_dev int32 [N]. */
+int eii_weight_colsum(const int8_t* W_dev, int N, int K, int32_t* wsum_dev, void* stream);
+
+/* Exact acc_dev int64 [M, N] = A W^T (python/intref.py:58-63 matmul_exact) with A_dev int16
+ * (a_bits 16) or int32 (a_bits 32) [M, K], W_dev int8 [N, K], K % 64 == 0. */
+int eii_gemm_i8(const void* A_dev, int a_bits, const int8_t* W_dev, int M, int N, int K,
+                int64_t* acc_dev, void* stream);
+/* The same with precomputed row sums (eii_weight_colsum). */
+int eii_gemm_i8_ws(const void* A_dev, int a_bits, const int8_t* W_dev, const int32_t* wsum_dev,
+                   int M, int N, int K, int64_t* acc_dev, void* stream);
+
+/* Linear with requantization (python/intref.py:186-190):
+ * out = SAT(RS(acc * mult[n], shift[n]), out_bits), shift[n] = n + f_in - f_out >= 1;
+ * out_dev int16 (out_bits 16) or int32 (out_bits 32) [M, N]. */
+int eii_linear(const void* A_dev, int a_bits, const int8_t* W_dev, const int32_t* wsum_dev,
+               const int32_t* mult_dev, const int32_t* shift_dev, int M, int N, int K,
+               int out_bits, void* out_dev, void* stream);
+
+/* RMSNorm (python/intref.py:168-184): x_dev int32 [M, 576] -> out_dev [M, 576] of out_bits
+ * (16 -> int16, 32 -> int32); gain_dev int32 [576] with exponent f_gain. */
+int eii_rmsnorm(const int32_t* x_dev, int M, const int32_t* gain_dev, int f_gain, int f_out,
+                int out_bits, void* out_dev, void* stream);
+
+/* Attention of one block (python/intref.py:227-254) for nseq sequences packed by
+ * seq_off_dev int32 [nseq + 1]: qkv_dev int16 [M, 960] holding q_rope | k_rope | v,
+ * exp_tab_dev int32 [1537]; ctx_dev [M, 576] of bits_c (16 -> int16, 32 -> int32). */
+int eii_attention(const int16_t* qkv_dev, const int32_t* seq_off_dev, int nseq, int max_T,
+                  const int32_t* exp_tab_dev, int f_qr, int f_kr, int f_v, int f_c, int bits_c,
+                  void* ctx_dev, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* EII_H */

@@ -1,0 +1,121 @@
+"""Operator parity of the HIP kernels with the oracle (exact integer equality)."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+from eii import lib as L
+from eii.tables import exp_table
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def p(t):
+    return C.c_void_p(t.data_ptr())
+
+
+def gemm(A, W):
+    lib = L.load()
+    a_bits = 16 if A.dtype == np.int16 else 32
+    M, K = A.shape
+    N = W.shape[0]
+    acc = torch.empty((M, N), dtype=torch.int64, device="cuda")
+    At, Wt = dev(A), dev(W)                          # keep the inputs alive until the kernel ran
+    L.check(lib.eii_gemm_i8(p(At), a_bits, p(Wt), M, N, K, p(acc), None))
+    torch.cuda.synchronize()
+    return acc.cpu().numpy()
+
+
+def exact_mm(A, W):
+    # float64 BLAS is exact while K * max|a| * 127 < 2^53 (python/intref.py:58-63)
+    assert A.shape[1] * 2.0 ** 31 * 127 < 2.0 ** 53
+    return np.rint(A.astype(np.float64) @ W.astype(np.float64).T).astype(np.int64)
+
+
+@pytest.mark.parametrize("a_dtype", [np.int16, np.int32])
+@pytest.mark.parametrize("M,N,K", [(1, 16, 64), (197, 80, 128), (130, 200, 576), (64, 576, 1536)])
+def test_gemm_small(a_dtype, M, N, K):
+    rng = np.random.default_rng(M * 1000 + N + K)
+    info = np.iinfo(a_dtype)
+    A = rng.integers(info.min, info.max, size=(M, K), endpoint=True, dtype=np.int64).astype(a_dtype)
+    A[0, :4] = [info.min, info.max, -1, 0]
+    W = rng.integers(-127, 128, size=(N, K), dtype=np.int8)
+    W[0, :3] = [-128, 127, -1]                       # the full int8 range, beyond model weights
+    got = gemm(A, W)
+    np.testing.assert_array_equal(got, exact_mm(A, W))
+
+
+def test_gemm_layout_probe():
+    # one-hot rows and columns: acc[m, n] picks single products, so a wrong lane/byte layout of
+    # the MFMA operands shows up as a misplaced entry rather than a different sum
+    M, N, K = 64, 64, 64
+    A = np.zeros((M, K), dtype=np.int16)
+    W = np.zeros((N, K), dtype=np.int8)
+    for m in range(M):
+        A[m, (5 * m + 3) % K] = 1000 + m
+    for n in range(N):
+        W[n, (5 * n + 3) % K] = 1 + (n % 100)
+    got = gemm(A, W)
+    np.testing.assert_array_equal(got, exact_mm(A, W))
+
+
+def test_rmsnorm(oracle):
+    lib = L.load()
+    rng = np.random.default_rng(7)
+    x = rng.integers(-2 ** 31, 2 ** 31, size=(37, 576), dtype=np.int64)
+    x[1] = -2 ** 31                                  # largest sum of squares
+    x[2] = 0                                         # only epsilon
+    x[3] = rng.integers(-3, 4, size=576)
+    x[4, :] = 0; x[4, 7] = 2 ** 31 - 1               # one element carries everything
+    x[5] = rng.integers(-2 ** 16, 2 ** 16, size=576)
+    gain = rng.integers(-2 ** 15, 2 ** 15, size=576, dtype=np.int64)
+    xt, gt = dev(x.astype(np.int32)), dev(gain.astype(np.int32))
+    for f_gain, f_out, bits in [(14, 13, 16), (14, 11, 16), (12, 20, 32), (14, 40, 16)]:
+        want = oracle.rmsnorm(x, (gain, f_gain), f_out, bits)
+        out = torch.empty((37, 576), dtype=torch.int16 if bits == 16 else torch.int32, device="cuda")
+        L.check(lib.eii_rmsnorm(p(xt), 37, p(gt), f_gain, f_out, bits, p(out), None))
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(out.cpu().numpy().astype(np.int64), want)
+
+
+def _attention_case(oracle, lens, scale, seed, f_qr=10, f_kr=9, f_v=11, f_c=11, bits_c=16):
+    lib = L.load()
+    rng = np.random.default_rng(seed)
+    M = sum(lens)
+    qkv = np.clip(np.round(rng.standard_normal((M, 960)) * scale), -32768, 32767).astype(np.int16)
+    off = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    E = exp_table().astype(np.int32)
+    ctx = torch.empty((M, 576), dtype=torch.int16 if bits_c == 16 else torch.int32, device="cuda")
+    qt, ot, et = dev(qkv), dev(off), dev(E)
+    L.check(lib.eii_attention(p(qt), p(ot), len(lens), max(lens), p(et), f_qr, f_kr, f_v, f_c, bits_c, p(ctx),
+                              None))
+    torch.cuda.synchronize()
+    got = ctx.cpu().numpy().astype(np.int64)
+    shift_s = f_qr + f_kr + 3 - 7
+    q = qkv[:, :576].astype(np.int64).reshape(M, 9, 64)
+    k = qkv[:, 576:768].astype(np.int64).reshape(M, 3, 64)
+    v = qkv[:, 768:].astype(np.int64).reshape(M, 3, 64)
+    for b in range(len(lens)):
+        sl = slice(off[b], off[b + 1])
+        want = oracle.attention(q[sl], k[sl], v[sl], shift_s, f_v, f_c, bits_c, 16, 16, 16)
+        np.testing.assert_array_equal(got[sl], want.reshape(-1, 576), err_msg=f"sequence {b}")
+
+
+@pytest.mark.parametrize("scale", [300.0, 2000.0])
+@pytest.mark.parametrize("lens", [[1], [64], [65, 3, 130], [160, 160]])
+def test_attention_spread(oracle, lens, scale):
+    _attention_case(oracle, lens, scale=scale, seed=len(lens))
+
+
+def test_attention_saturated(oracle):
+    # scores pinned at the 16-bit limits: many keys fall beyond the table (d > 1536), P = 65536 occurs
+    _attention_case(oracle, [150, 7], scale=20000.0, seed=3, f_qr=8, f_kr=8)
+
+
+def test_attention_ctx32(oracle):
+    _attention_case(oracle, [100], scale=3000.0, seed=5, f_c=27, bits_c=32)

@@ -101,7 +101,34 @@ struct eii_model {
   size_t seq_cap = 0;
   std::vector<int32_t> last_lens;
   int* flags = nullptr;            // [1]: 1 logit overflow, 2 token id out of range
+  // per-launch event timing between eii_profile_begin and eii_profile_end
+  bool prof = false;
+  std::vector<hipEvent_t> ev;      // start/stop pairs
+  std::vector<int> ev_kind;
+  size_t ev_used = 0;
 };
+
+namespace {
+// Records a start and stop event around the launches made in its scope, on their stream.
+struct ProfScope {
+  eii_model* m;
+  hipStream_t s;
+  size_t i = 0;
+  bool on;
+  ProfScope(eii_model* m_, int kind, hipStream_t s_) : m(m_), s(s_) {
+    on = m->prof && m->ev_used + 2 <= m->ev.size();
+    if (on) {
+      i = m->ev_used;
+      m->ev_used += 2;
+      m->ev_kind[i / 2] = kind;
+      (void)hipEventRecord(m->ev[i], s);
+    }
+  }
+  ~ProfScope() {
+    if (on) (void)hipEventRecord(m->ev[i + 1], s);
+  }
+};
+}  // namespace
 
 namespace {
 
@@ -365,6 +392,7 @@ extern "C" void eii_model_free(eii_model* m) {
   if (m->seq_off) (void)hipFree(m->seq_off);
   if (m->rope_owned) { (void)hipFree(m->rope_c); (void)hipFree(m->rope_s); }
   if (m->flags) (void)hipFree(m->flags);
+  for (hipEvent_t e : m->ev) (void)hipEventDestroy(e);
   if (m->dev) (void)hipFree(m->dev);
   delete m;
 }
@@ -470,40 +498,71 @@ hipError_t copy_cols(void* dst, int dst_w, const void* src, int src_w, int col0,
 int run_block(eii_model* m, int l, int32_t* x, int M, int nseq, int max_T, const eii_trace* tr, hipStream_t s) {
   const Layer& L = m->L[l];
   const int hb = L.bits[NORM1] / 8;
-  HIPCHK(rmsnorm(x, M, L.ln1, 21 + L.ln1_f - L.f[NORM1], L.bits[NORM1], m->h, hb, s));
+  {
+    ProfScope ps(m, EII_K_NORM, s);
+    HIPCHK(rmsnorm(x, M, L.ln1, 21 + L.ln1_f - L.f[NORM1], L.bits[NORM1], m->h, hb, s));
+  }
   if (tr && tr->norm1_out) HIPCHK(hipMemcpyAsync(tr->norm1_out, m->h, (size_t)M * kD * hb, hipMemcpyDeviceToDevice, s));
   int rc;
-  if ((rc = gemm_req(L.qkv, m->h, hb, M, m->qkv, 16, s))) return rc;
+  {
+    ProfScope ps(m, EII_K_GEMM_QKV, s);
+    if ((rc = gemm_req(L.qkv, m->h, hb, M, m->qkv, 16, s))) return rc;
+  }
   if (tr && tr->q_proj) HIPCHK(copy_cols(tr->q_proj, kD, m->qkv, kQKVN, 0, kD, 2, M, s));
   if (tr && tr->k_proj) HIPCHK(copy_cols(tr->k_proj, 192, m->qkv, kQKVN, kD, 192, 2, M, s));
   if (tr && tr->v_proj) HIPCHK(copy_cols(tr->v_proj, 192, m->qkv, kQKVN, kD + 192, 192, 2, M, s));
-  HIPCHK(rope(m->qkv, M, m->pos, m->rope_c, m->rope_s, 30 + L.f[QP] - L.f[QR], L.bits[QR], 30 + L.f[KP] - L.f[KR],
-              L.bits[KR], s));
+  {
+    ProfScope ps(m, EII_K_ROPE, s);
+    HIPCHK(rope(m->qkv, M, m->pos, m->rope_c, m->rope_s, 30 + L.f[QP] - L.f[QR], L.bits[QR],
+                30 + L.f[KP] - L.f[KR], L.bits[KR], s));
+  }
   if (tr && tr->q_rope) HIPCHK(copy_cols(tr->q_rope, kD, m->qkv, kQKVN, 0, kD, 2, M, s));
   if (tr && tr->k_rope) HIPCHK(copy_cols(tr->k_rope, 192, m->qkv, kQKVN, kD, 192, 2, M, s));
   AttnArgs a{m->qkv, m->seq_off, m->exp_tab, m->ctx, nseq, max_T, L.f[QR] + L.f[KR] + 3 - kFScore,
              16 + L.f[VP] - L.f[CTX], L.bits[CTX]};
   const int cb = L.bits[CTX] / 8;
-  HIPCHK(attention(a, cb, s));
+  {
+    ProfScope ps(m, EII_K_ATTN, s);
+    HIPCHK(attention(a, cb, s));
+  }
   if (tr && tr->attn_ctx) HIPCHK(hipMemcpyAsync(tr->attn_ctx, m->ctx, (size_t)M * kD * cb, hipMemcpyDeviceToDevice, s));
-  if ((rc = gemm_resid(L.o, m->ctx, cb, M, x, s))) return rc;
+  {
+    ProfScope ps(m, EII_K_GEMM_O, s);
+    if ((rc = gemm_resid(L.o, m->ctx, cb, M, x, s))) return rc;
+  }
   if (tr && tr->resid_mid) HIPCHK(hipMemcpyAsync(tr->resid_mid, x, (size_t)M * kD * 4, hipMemcpyDeviceToDevice, s));
   const int h2b = L.bits[NORM2] / 8;
-  HIPCHK(rmsnorm(x, M, L.ln2, 21 + L.ln2_f - L.f[NORM2], L.bits[NORM2], m->h, h2b, s));
+  {
+    ProfScope ps(m, EII_K_NORM, s);
+    HIPCHK(rmsnorm(x, M, L.ln2, 21 + L.ln2_f - L.f[NORM2], L.bits[NORM2], m->h, h2b, s));
+  }
   if (tr && tr->norm2_out) HIPCHK(hipMemcpyAsync(tr->norm2_out, m->h, (size_t)M * kD * h2b, hipMemcpyDeviceToDevice, s));
-  if ((rc = gemm_req(L.gu, m->h, h2b, M, m->gu, 16, s))) return rc;
+  {
+    ProfScope ps(m, EII_K_GEMM_GU, s);
+    if ((rc = gemm_req(L.gu, m->h, h2b, M, m->gu, 16, s))) return rc;
+  }
   if (tr && tr->gate_proj) HIPCHK(copy_cols(tr->gate_proj, kDFF, m->gu, 2 * kDFF, 0, kDFF, 2, M, s));
   if (tr && tr->up_proj) HIPCHK(copy_cols(tr->up_proj, kDFF, m->gu, 2 * kDFF, kDFF, kDFF, 2, M, s));
   const int gb = L.bits[GATED] / 8;
-  HIPCHK(silu_gate(m->gu, M, L.silu, L.f[SILU] + L.f[UP] - L.f_m, L.bits[GATED], m->gated, gb, s));
+  {
+    ProfScope ps(m, EII_K_SILU, s);
+    HIPCHK(silu_gate(m->gu, M, L.silu, L.f[SILU] + L.f[UP] - L.f_m, L.bits[GATED], m->gated, gb, s));
+  }
   if (tr && tr->mlp_gated) HIPCHK(hipMemcpyAsync(tr->mlp_gated, m->gated, (size_t)M * kDFF * gb, hipMemcpyDeviceToDevice, s));
-  if ((rc = gemm_resid(L.down, m->gated, gb, M, x, s))) return rc;
+  {
+    ProfScope ps(m, EII_K_GEMM_DOWN, s);
+    if ((rc = gemm_resid(L.down, m->gated, gb, M, x, s))) return rc;
+  }
   return EII_OK;
 }
 
 int run_final(eii_model* m, const int32_t* x, int M, int32_t* logits, hipStream_t s) {
-  HIPCHK(rmsnorm(x, M, m->fg, 21 + m->fg_f - m->f_y, 16, m->h, 2, s));
+  {
+    ProfScope ps(m, EII_K_NORM, s);
+    HIPCHK(rmsnorm(x, M, m->fg, 21 + m->fg_f - m->f_y, 16, m->h, 2, s));
+  }
   GemmArgs g{m->h, m->head.W, M, kV, kD, m->head.wsum, m->head.mult, m->head.shift, logits, 32, m->flags};
+  ProfScope ps(m, EII_K_GEMM_HEAD, s);
   HIPCHK(gemm(g, 2, EPI_LOGITS, s));
   return EII_OK;
 }
@@ -527,7 +586,10 @@ int forward_impl(eii_model* m, const int64_t* ids, const std::vector<int32_t>& l
   int rc;
   if ((rc = ensure_ws(m, M)) || (rc = set_batch(m, lens, s))) return rc;
   const int Mi = (int)M;
-  HIPCHK(embed(ids, Mi, m->emb_q, m->emb_m, m->emb_sh, m->x, m->flags, s));
+  {
+    ProfScope ps(m, EII_K_EMBED, s);
+    HIPCHK(embed(ids, Mi, m->emb_q, m->emb_m, m->emb_sh, m->x, m->flags, s));
+  }
   if (emb_out) HIPCHK(hipMemcpyAsync(emb_out, m->x, M * kD * 4, hipMemcpyDeviceToDevice, s));
   for (int l = 0; l < kNL; ++l) {
     if ((rc = run_block(m, l, m->x, Mi, (int)lens.size(), max_T, nullptr, s))) return rc;
@@ -551,6 +613,37 @@ extern "C" int eii_forward_packed(eii_model* m, const int64_t* ids, const int32_
   if (!m || !ids || !seq_lens || nseq <= 0) return fail(EII_E_ARG, "bad forward arguments");
   std::vector<int32_t> lens(seq_lens, seq_lens + nseq);
   return forward_impl(m, ids, lens, emb_out, res_out, logits, (hipStream_t)stream);
+}
+
+extern "C" int eii_profile_begin(eii_model* m, int max_launches) {
+  if (!m || max_launches <= 0) return fail(EII_E_ARG, "bad profile arguments");
+  HIPCHK(hipSetDevice(m->device));
+  const size_t need = 2 * (size_t)max_launches;
+  while (m->ev.size() < need) {
+    hipEvent_t e;
+    HIPCHK(hipEventCreate(&e));
+    m->ev.push_back(e);
+  }
+  m->ev_kind.assign(m->ev.size() / 2, -1);
+  m->ev_used = 0;
+  m->prof = true;
+  return EII_OK;
+}
+
+extern "C" int eii_profile_end(eii_model* m, void* stream, double* ms, int* launches) {
+  if (!m || !ms || !launches) return fail(EII_E_ARG, "bad profile arguments");
+  m->prof = false;
+  HIPCHK(hipStreamSynchronize((hipStream_t)stream));
+  for (int k = 0; k < EII_K_COUNT; ++k) { ms[k] = 0.0; launches[k] = 0; }
+  for (size_t i = 0; i < m->ev_used; i += 2) {
+    float t = 0.f;
+    HIPCHK(hipEventElapsedTime(&t, m->ev[i], m->ev[i + 1]));
+    const int k = m->ev_kind[i / 2];
+    if (k >= 0 && k < EII_K_COUNT) { ms[k] += t; launches[k] += 1; }
+  }
+  const int dropped = m->ev_used >= m->ev.size() ? 1 : 0;
+  m->ev_used = 0;
+  return dropped ? fail(EII_E_ARG, "profile buffer full: raise max_launches") : EII_OK;
 }
 
 extern "C" int eii_check(eii_model* m, void* stream) {

@@ -11,6 +11,8 @@ LIB_PATH = os.path.join(_HERE, "libeii.so")
 HOSTCHECK_PATH = os.path.join(_HERE, "libeii_hostcheck.so")
 
 EII_OK, EII_E_IO, EII_E_DEVICE, EII_E_BOUND, EII_E_ARG = 0, 2, 3, 4, 5
+KERNEL_KINDS = ("embed", "rmsnorm", "gemm_qkv", "rope", "attention", "gemm_o", "gemm_gate_up", "silu_gate",
+                "gemm_down", "gemm_head")
 
 vp, i32, i64p, i32p = C.c_void_p, C.c_int, C.POINTER(C.c_int64), C.POINTER(C.c_int32)
 
@@ -38,6 +40,8 @@ SIGNATURES = {
     "eii_forward": (i32, [vp, vp, i32, i32, vp, vp, vp, vp]),
     "eii_forward_packed": (i32, [vp, vp, i32p, i32, vp, vp, vp, vp]),
     "eii_check": (i32, [vp, vp]),
+    "eii_profile_begin": (i32, [vp, i32]),
+    "eii_profile_end": (i32, [vp, vp, C.POINTER(C.c_double), i32p]),
     "eii_block": (i32, [vp, i32, vp, i32, i32, C.POINTER(eii_trace), vp]),
     "eii_embed": (i32, [vp, vp, i32, vp, vp]),
     "eii_final": (i32, [vp, vp, i32, vp, vp]),

@@ -82,6 +82,20 @@ int eii_embed(eii_model* m, const int64_t* ids_dev, int M, int32_t* x_dev, void*
  * logits_dev int32 [M, 49152]. */
 int eii_final(eii_model* m, const int32_t* x_dev, int M, int32_t* logits_dev, void* stream);
 
+/* Kernel classes timed by eii_profile_begin/end. */
+enum {
+  EII_K_EMBED = 0, EII_K_NORM, EII_K_GEMM_QKV, EII_K_ROPE, EII_K_ATTN, EII_K_GEMM_O, EII_K_GEMM_GU,
+  EII_K_SILU, EII_K_GEMM_DOWN, EII_K_GEMM_HEAD, EII_K_COUNT
+};
+
+/* Time every kernel launch of the model's forward/block/final calls with a pair of HIP events
+ * recorded on the launch stream, for up to max_launches launches.  No counterpart in the
+ * reference (which times whole runs, c/intref.c:225,256; cuda/intref.cu:283,302-304). */
+int eii_profile_begin(eii_model* m, int max_launches);
+/* Waits for `stream` and returns the summed milliseconds and launch counts per kernel class
+ * into ms[EII_K_COUNT] and launches[EII_K_COUNT]; status 5 if launches were dropped. */
+int eii_profile_end(eii_model* m, void* stream, double* ms, int* launches);
+
 /* ---- operator level (python/intref.py functions) ---- */
 
 /* Row sums of int8 weights W_dev [N, K] into wsum_dev int32 [N]. */

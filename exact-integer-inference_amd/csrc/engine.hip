@@ -302,7 +302,7 @@ extern "C" int eii_model_load(const char* path, int device, eii_model** out) {
     O.down = {ar.take((size_t)576 * 1536), ar.take(4 * 576), ar.take(4 * 576), ar.take(4 * 576), 576, 1536};
     // matrix i -> (stack, row offset, f_in, f_out)
     const MatOff* dst[7] = {&O.qkv, &O.qkv, &O.qkv, &O.o, &O.gu, &O.gu, &O.down};
-    const int row0[7] = {0, 576, 768, 0, 0, 1536, 0};
+    const int row0[7] = {0, 576, 768, 0, 0, 32, 0};
     const int fin[7] = {L.f[NORM1], L.f[NORM1], L.f[NORM1], L.f[CTX], L.f[NORM2], L.f[NORM2], L.f_m};
     const int fout[7] = {L.f[QP], L.f[KP], L.f[VP], kFRes, L.f[GATE], L.f[UP], kFRes};
     static const char* names[7] = {"q", "k", "v", "o", "gate", "up", "down"};
@@ -311,14 +311,23 @@ extern "C" int eii_model_load(const char* path, int device, eii_model** out) {
       const uint8_t* wq = rd.bytes((size_t)N * K);
       const std::vector<int64_t> m = rd.vec(N), n = rd.vec(N);
       if (!rd.ok) { delete M; return fail(EII_E_IO, "short read in layer " + std::to_string(l)); }
-      memcpy(ar.host.data() + dst[i]->W + (size_t)row0[i] * K, wq, (size_t)N * K);
+      // stacked row of matrix row r: gate and up interleave in blocks of 32 rows
+      // ([gate 32b..32b+31 | up 32b..32b+31]) so one wave's block holds (gate j, up j) pairs
+      auto srow = [&](int r) { return (i == 4 || i == 5) ? 64 * (r / 32) + row0[i] + r % 32 : row0[i] + r; };
       std::vector<int64_t> sh(N);
       for (int r = 0; r < N; ++r) sh[r] = n[r] + fin[i] - fout[i];
       const std::string what = "layer " + std::to_string(l) + " " + names[i];
-      if ((rc = narrow32(m, (int32_t*)(ar.host.data() + dst[i]->mult) + row0[i], -(1 << 14), 1 << 14, what + " m")) ||
-          (rc = narrow32(sh, (int32_t*)(ar.host.data() + dst[i]->shift) + row0[i], 1, 62, what + " requant shift"))) {
+      std::vector<int32_t> m32(N), sh32(N);
+      if ((rc = narrow32(m, m32.data(), -(1 << 14), 1 << 14, what + " m")) ||
+          (rc = narrow32(sh, sh32.data(), 1, 62, what + " requant shift"))) {
         delete M;
         return rc;
+      }
+      for (int r = 0; r < N; ++r) {
+        const int sr = srow(r);
+        memcpy(ar.host.data() + dst[i]->W + (size_t)sr * K, wq + (size_t)r * K, K);
+        ((int32_t*)(ar.host.data() + dst[i]->mult))[sr] = m32[r];
+        ((int32_t*)(ar.host.data() + dst[i]->shift))[sr] = sh32[r];
       }
     }
     const std::vector<int64_t> silu = rd.vec(65536);
@@ -498,26 +507,28 @@ hipError_t copy_cols(void* dst, int dst_w, const void* src, int src_w, int col0,
 int run_block(eii_model* m, int l, int32_t* x, int M, int nseq, int max_T, const eii_trace* tr, hipStream_t s) {
   const Layer& L = m->L[l];
   const int hb = L.bits[NORM1] / 8;
+  int rc;
   {
     ProfScope ps(m, EII_K_NORM, s);
     HIPCHK(rmsnorm(x, M, L.ln1, 21 + L.ln1_f - L.f[NORM1], L.bits[NORM1], m->h, hb, s));
   }
   if (tr && tr->norm1_out) HIPCHK(hipMemcpyAsync(tr->norm1_out, m->h, (size_t)M * kD * hb, hipMemcpyDeviceToDevice, s));
-  int rc;
-  {
+  const int sh_q = 30 + L.f[QP] - L.f[QR], sh_k = 30 + L.f[KP] - L.f[KR];
+  if (!tr) {
+    // q, k, v projections with RoPE applied in the epilogue
     ProfScope ps(m, EII_K_GEMM_QKV, s);
+    GemmArgs g{m->h, L.qkv.W, M, L.qkv.N, L.qkv.K, L.qkv.wsum, L.qkv.mult, L.qkv.shift, m->qkv, 16, nullptr};
+    g.pos = m->pos; g.cosT = m->rope_c; g.sinT = m->rope_s; g.sh_q = sh_q; g.sh_k = sh_k;
+    HIPCHK(gemm(g, hb, EPI_QKV, s));
+  } else {
     if ((rc = gemm_req(L.qkv, m->h, hb, M, m->qkv, 16, s))) return rc;
+    if (tr->q_proj) HIPCHK(copy_cols(tr->q_proj, kD, m->qkv, kQKVN, 0, kD, 2, M, s));
+    if (tr->k_proj) HIPCHK(copy_cols(tr->k_proj, 192, m->qkv, kQKVN, kD, 192, 2, M, s));
+    if (tr->v_proj) HIPCHK(copy_cols(tr->v_proj, 192, m->qkv, kQKVN, kD + 192, 192, 2, M, s));
+    HIPCHK(rope(m->qkv, M, m->pos, m->rope_c, m->rope_s, sh_q, L.bits[QR], sh_k, L.bits[KR], s));
+    if (tr->q_rope) HIPCHK(copy_cols(tr->q_rope, kD, m->qkv, kQKVN, 0, kD, 2, M, s));
+    if (tr->k_rope) HIPCHK(copy_cols(tr->k_rope, 192, m->qkv, kQKVN, kD, 192, 2, M, s));
   }
-  if (tr && tr->q_proj) HIPCHK(copy_cols(tr->q_proj, kD, m->qkv, kQKVN, 0, kD, 2, M, s));
-  if (tr && tr->k_proj) HIPCHK(copy_cols(tr->k_proj, 192, m->qkv, kQKVN, kD, 192, 2, M, s));
-  if (tr && tr->v_proj) HIPCHK(copy_cols(tr->v_proj, 192, m->qkv, kQKVN, kD + 192, 192, 2, M, s));
-  {
-    ProfScope ps(m, EII_K_ROPE, s);
-    HIPCHK(rope(m->qkv, M, m->pos, m->rope_c, m->rope_s, 30 + L.f[QP] - L.f[QR], L.bits[QR],
-                30 + L.f[KP] - L.f[KR], L.bits[KR], s));
-  }
-  if (tr && tr->q_rope) HIPCHK(copy_cols(tr->q_rope, kD, m->qkv, kQKVN, 0, kD, 2, M, s));
-  if (tr && tr->k_rope) HIPCHK(copy_cols(tr->k_rope, 192, m->qkv, kQKVN, kD, 192, 2, M, s));
   AttnArgs a{m->qkv, m->seq_off, m->exp_tab, m->ctx, nseq, max_T, L.f[QR] + L.f[KR] + 3 - kFScore,
              16 + L.f[VP] - L.f[CTX], L.bits[CTX]};
   const int cb = L.bits[CTX] / 8;
@@ -537,16 +548,23 @@ int run_block(eii_model* m, int l, int32_t* x, int M, int nseq, int max_T, const
     HIPCHK(rmsnorm(x, M, L.ln2, 21 + L.ln2_f - L.f[NORM2], L.bits[NORM2], m->h, h2b, s));
   }
   if (tr && tr->norm2_out) HIPCHK(hipMemcpyAsync(tr->norm2_out, m->h, (size_t)M * kD * h2b, hipMemcpyDeviceToDevice, s));
-  {
-    ProfScope ps(m, EII_K_GEMM_GU, s);
-    if ((rc = gemm_req(L.gu, m->h, h2b, M, m->gu, 16, s))) return rc;
-  }
-  if (tr && tr->gate_proj) HIPCHK(copy_cols(tr->gate_proj, kDFF, m->gu, 2 * kDFF, 0, kDFF, 2, M, s));
-  if (tr && tr->up_proj) HIPCHK(copy_cols(tr->up_proj, kDFF, m->gu, 2 * kDFF, kDFF, kDFF, 2, M, s));
   const int gb = L.bits[GATED] / 8;
-  {
-    ProfScope ps(m, EII_K_SILU, s);
-    HIPCHK(silu_gate(m->gu, M, L.silu, L.f[SILU] + L.f[UP] - L.f_m, L.bits[GATED], m->gated, gb, s));
+  const int sh_s = L.f[SILU] + L.f[UP] - L.f_m;
+  if (!tr) {
+    // gate and up projections with the SiLU table and the gated product in the epilogue
+    ProfScope ps(m, EII_K_GEMM_GU, s);
+    GemmArgs g{m->h, L.gu.W, M, L.gu.N, L.gu.K, L.gu.wsum, L.gu.mult, L.gu.shift, m->gated, 16, nullptr};
+    g.aux_tab = L.silu; g.sh2 = sh_s; g.bits2 = L.bits[GATED];
+    HIPCHK(gemm(g, h2b, EPI_SILU, s));
+  } else {
+    if ((rc = gemm_req(L.gu, m->h, h2b, M, m->gu, 16, s))) return rc;
+    // gu holds [gate 32 | up 32] blocks; de-interleave for the dumps
+    if (tr->gate_proj)
+      HIPCHK(hipMemcpy2DAsync(tr->gate_proj, 64, m->gu, 128, 64, (size_t)M * 48, hipMemcpyDeviceToDevice, s));
+    if (tr->up_proj)
+      HIPCHK(hipMemcpy2DAsync(tr->up_proj, 64, (const uint8_t*)m->gu + 64, 128, 64, (size_t)M * 48,
+                              hipMemcpyDeviceToDevice, s));
+    HIPCHK(silu_gate(m->gu, M, L.silu, sh_s, L.bits[GATED], m->gated, gb, s));
   }
   if (tr && tr->mlp_gated) HIPCHK(hipMemcpyAsync(tr->mlp_gated, m->gated, (size_t)M * kDFF * gb, hipMemcpyDeviceToDevice, s));
   {

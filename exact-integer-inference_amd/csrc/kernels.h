@@ -12,6 +12,12 @@ enum Epi : int {
   EPI_REQ32 = 2,   // out int32 [M, N] = SAT(RS(acc * m[n], sh[n]), sat_bits)
   EPI_RESID = 3,   // x int32 [M, N] = SAT32(x + RS(acc * m[n], sh[n]))
   EPI_LOGITS = 4,  // out int32 [M, N] = RS(acc * m[n], sh[n]); *flag |= 1 if it leaves int32
+  // W = blocks of [32 gate rows | 32 up rows] (N = 2 * 1536): out [M, N/2] of bits2 =
+  //   SAT(RS(aux_tab[SAT16(gate) + 32768] * SAT16(up), sh2), bits2)        (python/intref.py:268-275)
+  EPI_SILU = 5,
+  // W = q | k | v rows (N = 960, 16-bit outputs): RoPE on q heads (shift sh_q) and k heads (sh_k)
+  // at positions pos[m] with cosT/sinT [rows, 32], out int16 [M, 960]        (python/intref.py:207-222)
+  EPI_QKV = 6,
 };
 
 struct GemmArgs {
@@ -24,6 +30,14 @@ struct GemmArgs {
   void* out;
   int sat_bits;
   int* flag;
+  // EPI_SILU
+  const int32_t* aux_tab = nullptr;
+  int sh2 = 0, bits2 = 16;
+  // EPI_QKV
+  const int32_t* pos = nullptr;
+  const int32_t* cosT = nullptr;
+  const int32_t* sinT = nullptr;
+  int sh_q = 0, sh_k = 0;
 };
 
 hipError_t gemm(const GemmArgs& a, int a_bytes, int epi, hipStream_t s);
@@ -41,7 +55,8 @@ hipError_t rmsnorm(const int32_t* x, int M, const int32_t* gain, int sh_out, int
 hipError_t rope(int16_t* qkv, int M, const int32_t* pos, const int32_t* cosT, const int32_t* sinT,
                 int sh_q, int bits_q, int sh_k, int bits_k, hipStream_t s);
 
-// gated[m, j] = SAT(RS(silu[gu[m, j] + 32768] * gu[m, 1536 + j], sh), bits)
+// gated[m, j] = SAT(RS(silu[gate + 32768] * up, sh), bits) with gu rows holding [gate 32 | up 32]
+// blocks: gate j at column 64 (j / 32) + j % 32, up j 32 columns further
 hipError_t silu_gate(const int16_t* gu, int M, const int32_t* silu, int sh, int bits,
                      void* gated, int out_bytes, hipStream_t s);
 

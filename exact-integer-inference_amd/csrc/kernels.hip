@@ -39,70 +39,127 @@ __device__ __forceinline__ uint32_t byte_plane32(uint4 d, int i) {
 }
 
 // ------------------------------------------------------------------------------ GEMM
-template <int AW, int BM, int BN, int WM, int WN>
+// Workgroup = 8 waves over a BM x 128 output tile (BM = 256 for 2-limb activations, 128 for
+// 4-limb), K step 64, two LDS stages fed through registers.  The MFMA runs with the weights as
+// the A operand and the activations as the B operand, D[n][m] = sum_k W[n,k] a[m,k]: a lane
+// then holds four output columns n = 4*(lane/16)+r of one row m = lane%16 per 16x16 tile.  The
+// order of the weight rows inside a wave's 64-column block is free, so it is chosen per
+// epilogue (col_perm) to give each lane 16 consecutive columns (contiguous stores), or the
+// (gate j, up j) and RoPE (d, d+32) pairs in one lane.
+//
+// Epilogue arithmetic for 2-limb inputs runs in float64 and is exact: with P1, P0 the limb
+// partial sums (|P| < 2^25 for K <= 1536) and |m| <= 2^14,
+//   acc * m / 2^sh + 2^-(sh+1) = P1 * (256 m / 2^sh) + P0 * (m / 2^sh) + (128 wsum m / 2^sh + 2^-(sh+1))
+// is a sum of multiples of 2^-(sh+1) below 2^(49-sh), i.e. at most 50 significant bits, so both
+// FMAs are exact, and round-to-nearest-even of that value is RS(acc * m, sh) (the 2^-(sh+1)
+// offset turns the reference's round-half-up into a tie-free rounding).  4-limb inputs, whose
+// acc * m reaches 2^62, use int64.
+constexpr double kMagic = 6755399441055744.0;   // 1.5 * 2^52: y + kMagic rounds y to an integer
+
+__device__ __forceinline__ int32_t rne_i32(double y) {   // |y| < 2^31 after clamping
+  return (int32_t)(uint32_t)(uint64_t)__double_as_longlong(y + kMagic);
+}
+
+struct ColC { double c0, c1, cb; };
+__device__ __forceinline__ ColC col_coef(int32_t mu, int sh, int32_t ws) {
+  ColC k;
+  k.c0 = ldexp((double)mu, -sh);
+  k.c1 = k.c0 * 256.0;
+  k.cb = fma((double)ws * 128.0, k.c0, ldexp(0.5, -sh));   // per-column shifts are >= 1
+  return k;
+}
+// acc * m / 2^sh + 2^-(sh+1) for acc = 256 P1 + P0 + 128 wsum (exact, see above)
+__device__ __forceinline__ double req2(int32_t P1, int32_t P0, const ColC& k) {
+  return fma((double)P1, k.c1, fma((double)P0, k.c0, k.cb));
+}
+// SAT(RS(x, sh), bits) for an integer-valued double x with |x| < 2^52 (scalar shift, any sign)
+__device__ __forceinline__ int32_t rs_sat_f64(double x, int sh, double lo, double hi) {
+  const double y = sh >= 1 ? fma(x, ldexp(1.0, -sh), ldexp(0.5, -sh)) : x * ldexp(1.0, -sh);
+  return rne_i32(fmin(fmax(y, lo), hi));
+}
+
+enum Perm { PERM_CONTIG = 0, PERM_PAIR = 1 };
+// Row of a wave's 64-column weight block held at (n-tile t, lane group g, register r).
+template <int P>
+__device__ __forceinline__ int col_perm(int t, int g, int r) {
+  if constexpr (P == PERM_CONTIG) return 16 * g + 4 * t + r;           // lane g: columns 16g..16g+15
+  else return 32 * (t >> 1) + 8 * g + 4 * (t & 1) + r;                 // lane g: 8g..8g+7 and 32+8g..
+}
+
+template <int AW>
 struct GemmCfg {
+  static constexpr int BM = AW == 2 ? 256 : 128, BN = 128;
+  static constexpr int kWavesN = 2, WM = BM / 4, WN = 64;
+  static constexpr int TM = WM / 16, TN = 4;
   static constexpr int kPlane = BM * kLdsRow;
   static constexpr int kABytes = AW * kPlane;
-  static constexpr int kBBytes = BN * kLdsRow;
-  static constexpr int kStage = kABytes + kBBytes;
-  static constexpr int TM = WM / 16, TN = WN / 16;
-  static constexpr int kWavesN = BN / WN;
-  static constexpr int kAChunks = BM * 4 * AW / 256;   // 16-byte global loads per thread
-  static constexpr int kBChunks = BN * 4 / 256;
-  static_assert((BM / WM) * (BN / WN) == 4, "four waves per workgroup");
-  static_assert(kAChunks * 256 == BM * 4 * AW && kBChunks * 256 == BN * 4, "chunk split");
+  static constexpr int kStage = kABytes + BN * kLdsRow;
+  static constexpr int kAChunks = BM * 4 * AW / 512;   // 16-byte global loads per thread
+  static_assert(kAChunks * 512 == BM * 4 * AW, "A chunk split");
 };
 
-template <int AW, int BM, int BN, int WM, int WN, int EPI>
-__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
-  using C = GemmCfg<AW, BM, BN, WM, WN>;
+template <int EPI> struct EpiPerm { static constexpr int P = (EPI == EPI_SILU || EPI == EPI_QKV) ? PERM_PAIR : PERM_CONTIG; };
+
+// Tile of a workgroup: XCD x (= blockIdx % 8, the hardware's round-robin) takes a contiguous
+// range of tiles in grouped order (8 row blocks x all column blocks), so concurrently running
+// workgroups of one XCD share activation rows and weight blocks in that XCD's L2.
+__device__ __forceinline__ bool tile_of(int nMB, int nNB, int& mb, int& nb) {
+  const int nT = nMB * nNB, per = (nT + 7) / 8;
+  const int v = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+  if (v >= nT) return false;
+  const int G = 8, grp = v / (G * nNB), first = grp * G;
+  const int gs = min(nMB - first, G), in = v - grp * G * nNB;
+  mb = first + in % gs;
+  nb = in / gs;
+  return true;
+}
+
+template <int AW, int EPI>
+__global__ __launch_bounds__(512) void gemm_kernel(GemmArgs g) {
+  using C = GemmCfg<AW>;
+  constexpr int P = EpiPerm<EPI>::P;
   __shared__ __attribute__((aligned(16))) uint8_t smem[2 * C::kStage];
+  int mb, nb;
+  if (!tile_of((g.M + C::BM - 1) / C::BM, (g.N + C::BN - 1) / C::BN, mb, nb)) return;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave / C::kWavesN, wn = wave % C::kWavesN;
-  const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int m0 = mb * C::BM, n0 = nb * C::BN;
   const int nk = g.K / kBK;
   const uint8_t* Ab = (const uint8_t*)g.A;
 
-  uint4 areg[C::kAChunks], breg[C::kBChunks];
+  // this thread's weight row (permuted within its 64-row block) and 16-byte chunk
+  const int wj = tid >> 2, wc = tid & 3;
+  const int wrow = n0 + (wj & 64) + col_perm<P>((wj & 63) >> 4, (wj & 15) >> 2, wj & 3);
+  const int8_t* wsrc = wrow < g.N ? g.W + (size_t)wrow * g.K + wc * 16 : nullptr;
 
+  uint4 areg[C::kAChunks], breg;
   auto load = [&](int kb) {
 #pragma unroll
     for (int i = 0; i < C::kAChunks; ++i) {
-      const int q = tid + 256 * i, row = q / (4 * AW), c = q % (4 * AW);
-      const int m = m0 + row;
+      const int q = tid + 512 * i, row = q / (4 * AW), c = q % (4 * AW), m = m0 + row;
       areg[i] = m < g.M ? *(const uint4*)(Ab + ((size_t)m * g.K + (size_t)kb * kBK) * AW + c * 16)
                         : make_uint4(0, 0, 0, 0);
     }
-#pragma unroll
-    for (int i = 0; i < C::kBChunks; ++i) {
-      const int q = tid + 256 * i, row = q / 4, c = q % 4;
-      const int n = n0 + row;
-      breg[i] = n < g.N ? *(const uint4*)(g.W + (size_t)n * g.K + (size_t)kb * kBK + c * 16)
-                        : make_uint4(0, 0, 0, 0);
-    }
+    breg = wsrc ? *(const uint4*)(wsrc + (size_t)kb * kBK) : make_uint4(0, 0, 0, 0);
   };
   auto store = [&](int st) {
     uint8_t* base = smem + st * C::kStage;
 #pragma unroll
     for (int i = 0; i < C::kAChunks; ++i) {
-      const int q = tid + 256 * i, row = q / (4 * AW), c = q % (4 * AW);
+      const int q = tid + 512 * i, row = q / (4 * AW), c = q % (4 * AW);
       const uint4 d = areg[i];
       if constexpr (AW == 2) {
-        uint8_t* p = base + row * kLdsRow + c * 8;       // 8 elements -> 8 bytes per plane
+        uint8_t* p = base + row * kLdsRow + c * 8;
         *(uint2*)(p) = make_uint2(lo_bytes16(d.x, d.y), lo_bytes16(d.z, d.w));
         *(uint2*)(p + C::kPlane) = make_uint2(hi_bytes16(d.x, d.y), hi_bytes16(d.z, d.w));
       } else {
-        uint8_t* p = base + row * kLdsRow + c * 4;       // 4 elements -> 4 bytes per plane
+        uint8_t* p = base + row * kLdsRow + c * 4;
 #pragma unroll
         for (int pl = 0; pl < 4; ++pl) *(uint32_t*)(p + pl * C::kPlane) = byte_plane32(d, pl);
       }
     }
-#pragma unroll
-    for (int i = 0; i < C::kBChunks; ++i) {
-      const int q = tid + 256 * i, row = q / 4, c = q % 4;
-      *(uint4*)(base + C::kABytes + row * kLdsRow + c * 16) = breg[i];
-    }
+    *(uint4*)(base + C::kABytes + wj * kLdsRow + wc * 16) = breg;
   };
 
   v4i acc[C::TM][C::TN][AW];
@@ -121,57 +178,212 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
     const int cur = kb & 1;
     if (kb + 1 < nk) load(kb + 1);
     const uint8_t* base = smem + cur * C::kStage;
-    v4i bf[C::TN];
+    v4i wf[C::TN];
 #pragma unroll
     for (int tn = 0; tn < C::TN; ++tn)
-      bf[tn] = *(const v4i*)(base + C::kABytes + (wn * WN + tn * 16 + fr) * kLdsRow + fk);
+      wf[tn] = *(const v4i*)(base + C::kABytes + (wn * C::WN + tn * 16 + fr) * kLdsRow + fk);
 #pragma unroll
     for (int tm = 0; tm < C::TM; ++tm) {
 #pragma unroll
       for (int l = 0; l < AW; ++l) {
-        const v4i af = *(const v4i*)(base + l * C::kPlane + (wm * WM + tm * 16 + fr) * kLdsRow + fk);
+        const v4i af = *(const v4i*)(base + l * C::kPlane + (wm * C::WM + tm * 16 + fr) * kLdsRow + fk);
 #pragma unroll
-        for (int tn = 0; tn < C::TN; ++tn) acc[tm][tn][l] = mfma(af, bf[tn], acc[tm][tn][l]);
+        for (int tn = 0; tn < C::TN; ++tn) acc[tm][tn][l] = mfma(wf[tn], af, acc[tm][tn][l]);
       }
     }
     if (kb + 1 < nk) store(cur ^ 1);
     __syncthreads();
   }
 
-  // Epilogue: lane holds rows 4*(lane/16)+r, column lane%16 of each 16x16 tile.
-  const int64_t bias = limb_bias(AW);
+  // ---------------------------------------------------------------- epilogue
+  const int gq = lane >> 4;
+  const int nblk = n0 + wn * C::WN;                     // first column of this wave's block
+  int mrow[C::TM];
 #pragma unroll
-  for (int tn = 0; tn < C::TN; ++tn) {
-    const int n = n0 + wn * WN + tn * 16 + fr;
-    if (n >= g.N) continue;
-    const int64_t cw = bias * (int64_t)g.wsum[n];
-    int32_t mu = 0, sh = 1;
-    if constexpr (EPI != EPI_I64) { mu = g.mult[n]; sh = g.shift[n]; }
+  for (int tm = 0; tm < C::TM; ++tm) mrow[tm] = m0 + wm * C::WM + tm * 16 + fr;
+
+  if constexpr (EPI == EPI_I64 || EPI == EPI_REQ16 || EPI == EPI_REQ32 || EPI == EPI_RESID || EPI == EPI_LOGITS) {
+    // PERM_CONTIG: lane holds columns nblk + 16 gq + 4 t + r
+    const double lo = EPI == EPI_REQ16 || EPI == EPI_REQ32 ? -ldexp(1.0, g.sat_bits - 1) : 0.0;
+    const double hi = EPI == EPI_REQ16 || EPI == EPI_REQ32 ? ldexp(1.0, g.sat_bits - 1) - 1.0 : 0.0;
 #pragma unroll
-    for (int tm = 0; tm < C::TM; ++tm) {
+    for (int t = 0; t < C::TN; ++t) {
+      const int nc = nblk + 16 * gq + 4 * t;           // 4 consecutive columns nc..nc+3
+      if (nc >= g.N) continue;                          // N is a multiple of 4
+      const int4 ws4 = *(const int4*)(g.wsum + nc);
+      int4 mu4 = make_int4(0, 0, 0, 0), sh4 = make_int4(1, 1, 1, 1);
+      if constexpr (EPI != EPI_I64) { mu4 = *(const int4*)(g.mult + nc); sh4 = *(const int4*)(g.shift + nc); }
+      const int wsv[4] = {ws4.x, ws4.y, ws4.z, ws4.w}, muv[4] = {mu4.x, mu4.y, mu4.z, mu4.w},
+                shv[4] = {sh4.x, sh4.y, sh4.z, sh4.w};
+      if constexpr (AW == 2 && EPI != EPI_I64) {
+        ColC k[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = m0 + wm * WM + tm * 16 + (lane >> 4) * 4 + r;
-        if (m >= g.M) continue;
-        int64_t a = cw;
+        for (int r = 0; r < 4; ++r) k[r] = col_coef(muv[r], shv[r], wsv[r]);
 #pragma unroll
-        for (int l = 0; l < AW; ++l) a += (int64_t)acc[tm][tn][l][r] * ((int64_t)1 << (8 * l));
-        const size_t o = (size_t)m * g.N + n;
-        if constexpr (EPI == EPI_I64) {
-          ((int64_t*)g.out)[o] = a;
-        } else {
-          const int64_t v = rs(a * mu, sh);
+        for (int tm = 0; tm < C::TM; ++tm) {
+          const int m = mrow[tm];
+          if (m >= g.M) continue;
+          const size_t o = (size_t)m * g.N + nc;
+          double y[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) y[r] = req2(acc[tm][t][1][r], acc[tm][t][0][r], k[r]);
           if constexpr (EPI == EPI_REQ16) {
-            ((int16_t*)g.out)[o] = (int16_t)sat(v, g.sat_bits);
+            int v[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[r] = rne_i32(fmin(fmax(y[r], lo), hi));
+            *(uint2*)((int16_t*)g.out + o) = make_uint2((uint32_t)(v[0] & 0xFFFF) | ((uint32_t)v[1] << 16),
+                                                       (uint32_t)(v[2] & 0xFFFF) | ((uint32_t)v[3] << 16));
           } else if constexpr (EPI == EPI_REQ32) {
-            ((int32_t*)g.out)[o] = (int32_t)sat(v, g.sat_bits);
+            int4 v;
+            v.x = rne_i32(fmin(fmax(y[0], lo), hi)); v.y = rne_i32(fmin(fmax(y[1], lo), hi));
+            v.z = rne_i32(fmin(fmax(y[2], lo), hi)); v.w = rne_i32(fmin(fmax(y[3], lo), hi));
+            *(int4*)((int32_t*)g.out + o) = v;
           } else if constexpr (EPI == EPI_RESID) {
-            int32_t* x = (int32_t*)g.out;
-            x[o] = (int32_t)clamp_bits32((int64_t)x[o] + v);
-          } else {
-            if (v != (int64_t)(int32_t)v) atomicOr(g.flag, 1);
-            ((int32_t*)g.out)[o] = (int32_t)v;
+            int4* xp = (int4*)((int32_t*)g.out + o);
+            const int4 x = *xp;
+            const double xv[4] = {(double)x.x, (double)x.y, (double)x.z, (double)x.w};
+            int v[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              v[r] = rne_i32(fmin(fmax(rint(y[r]) + xv[r], -2147483648.0), 2147483647.0));
+            *xp = make_int4(v[0], v[1], v[2], v[3]);
+          } else {   // EPI_LOGITS
+            int v[4];
+            bool bad = false;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const double t2 = rint(y[r]);
+              bad |= t2 > 2147483647.0 || t2 < -2147483648.0;
+              v[r] = rne_i32(t2);
+            }
+            if (bad) atomicOr(g.flag, 1);
+            *(int4*)((int32_t*)g.out + o) = make_int4(v[0], v[1], v[2], v[3]);
           }
+        }
+      } else {
+        const int64_t bias = limb_bias(AW);
+#pragma unroll
+        for (int tm = 0; tm < C::TM; ++tm) {
+          const int m = mrow[tm];
+          if (m >= g.M) continue;
+          const size_t o = (size_t)m * g.N + nc;
+          int64_t a[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            a[r] = bias * (int64_t)wsv[r];
+#pragma unroll
+            for (int l = 0; l < AW; ++l) a[r] += (int64_t)acc[tm][t][l][r] * ((int64_t)1 << (8 * l));
+          }
+          if constexpr (EPI == EPI_I64) {
+            int64_t* op = (int64_t*)g.out + o;
+            *(longlong2*)op = make_longlong2(a[0], a[1]);
+            *(longlong2*)(op + 2) = make_longlong2(a[2], a[3]);
+          } else {
+            int64_t v[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[r] = rs(a[r] * muv[r], shv[r]);
+            if constexpr (EPI == EPI_REQ16) {
+              *(uint2*)((int16_t*)g.out + o) =
+                  make_uint2((uint32_t)(sat(v[0], g.sat_bits) & 0xFFFF) | ((uint32_t)sat(v[1], g.sat_bits) << 16),
+                             (uint32_t)(sat(v[2], g.sat_bits) & 0xFFFF) | ((uint32_t)sat(v[3], g.sat_bits) << 16));
+            } else if constexpr (EPI == EPI_REQ32) {
+              *(int4*)((int32_t*)g.out + o) = make_int4((int)sat(v[0], g.sat_bits), (int)sat(v[1], g.sat_bits),
+                                                        (int)sat(v[2], g.sat_bits), (int)sat(v[3], g.sat_bits));
+            } else if constexpr (EPI == EPI_RESID) {
+              int4* xp = (int4*)((int32_t*)g.out + o);
+              const int4 x = *xp;
+              *xp = make_int4((int)clamp_bits32((int64_t)x.x + v[0]), (int)clamp_bits32((int64_t)x.y + v[1]),
+                              (int)clamp_bits32((int64_t)x.z + v[2]), (int)clamp_bits32((int64_t)x.w + v[3]));
+            } else {
+              bool bad = false;
+#pragma unroll
+              for (int r = 0; r < 4; ++r) bad |= v[r] != (int64_t)(int32_t)v[r];
+              if (bad) atomicOr(g.flag, 1);
+              *(int4*)((int32_t*)g.out + o) = make_int4((int)v[0], (int)v[1], (int)v[2], (int)v[3]);
+            }
+          }
+        }
+      }
+    }
+  } else {
+    // PERM_PAIR: lane holds block-local rows j = 8 gq + 4 (t & 1) + r (t = 0, 1) paired with j + 32
+    // (t = 2, 3): (gate j, up j) for EPI_SILU, (d, d + 32) of one head for EPI_QKV.
+    const int64_t bias = limb_bias(AW);
+    auto value16 = [&](int tm, int t, int r, int n) -> int32_t {   // SAT16(RS(acc * m, sh)) of column n
+      if constexpr (AW == 2) {
+        const ColC k = col_coef(g.mult[n], g.shift[n], g.wsum[n]);
+        return rne_i32(fmin(fmax(req2(acc[tm][t][1][r], acc[tm][t][0][r], k), -32768.0), 32767.0));
+      } else {
+        int64_t a = bias * (int64_t)g.wsum[n];
+#pragma unroll
+        for (int l = 0; l < AW; ++l) a += (int64_t)acc[tm][t][l][r] * ((int64_t)1 << (8 * l));
+        return (int32_t)clamp_bits16(rs(a * g.mult[n], g.shift[n]));
+      }
+    };
+    if constexpr (EPI == EPI_SILU) {
+      // gated[m, j]: j = 32 * (nblk / 64) + 8 gq + 4 t + r, t = 0, 1; weight rows nblk + j' and nblk + 32 + j'
+      const int jb = (nblk >> 6) * 32 + 8 * gq;
+      const double lo = -ldexp(1.0, g.bits2 - 1), hi = ldexp(1.0, g.bits2 - 1) - 1.0;
+      if (nblk < g.N) {
+#pragma unroll
+        for (int tm = 0; tm < C::TM; ++tm) {
+          const int m = mrow[tm];
+          if (m >= g.M) continue;
+          int32_t v[8];
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int jl = 8 * gq + 4 * t + r;
+              const int32_t gv = value16(tm, t, r, nblk + jl);
+              const int32_t uv = value16(tm, t + 2, r, nblk + 32 + jl);
+              const double sg = (double)g.aux_tab[gv + 32768];
+              v[4 * t + r] = rs_sat_f64(sg * (double)uv, g.sh2, lo, hi);
+            }
+          const size_t o = (size_t)m * (g.N / 2) + jb;
+          if (g.bits2 == 16) {
+            *(uint4*)((int16_t*)g.out + o) = make_uint4(
+                (uint32_t)(v[0] & 0xFFFF) | ((uint32_t)v[1] << 16), (uint32_t)(v[2] & 0xFFFF) | ((uint32_t)v[3] << 16),
+                (uint32_t)(v[4] & 0xFFFF) | ((uint32_t)v[5] << 16), (uint32_t)(v[6] & 0xFFFF) | ((uint32_t)v[7] << 16));
+          } else {
+            *(int4*)((int32_t*)g.out + o) = make_int4(v[0], v[1], v[2], v[3]);
+            *(int4*)((int32_t*)g.out + o + 4) = make_int4(v[4], v[5], v[6], v[7]);
+          }
+        }
+      }
+    } else {   // EPI_QKV: heads 0..8 q and 9..11 k get RoPE, 12..14 v are stored as they are
+      const int head = nblk >> 6;
+      if (nblk < g.N) {
+        const int shr = head < 9 ? g.sh_q : g.sh_k;
+#pragma unroll
+        for (int tm = 0; tm < C::TM; ++tm) {
+          const int m = mrow[tm];
+          if (m >= g.M) continue;
+          int32_t lo8[8], hi8[8];
+          const int ps = head < 12 ? g.pos[m] : 0;
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int d = 8 * gq + 4 * t + r;
+              const int32_t a1 = value16(tm, t, r, nblk + d), a2 = value16(tm, t + 2, r, nblk + 32 + d);
+              if (head < 12) {
+                const double c = (double)g.cosT[ps * 32 + d], s = (double)g.sinT[ps * 32 + d];
+                const double o1 = fma((double)a1, c, -(double)a2 * s), o2 = fma((double)a2, c, (double)a1 * s);
+                lo8[4 * t + r] = rs_sat_f64(o1, shr, -32768.0, 32767.0);
+                hi8[4 * t + r] = rs_sat_f64(o2, shr, -32768.0, 32767.0);
+              } else {
+                lo8[4 * t + r] = a1;
+                hi8[4 * t + r] = a2;
+              }
+            }
+          int16_t* op = (int16_t*)g.out + (size_t)m * g.N + nblk + 8 * gq;
+          *(uint4*)op = make_uint4(
+              (uint32_t)(lo8[0] & 0xFFFF) | ((uint32_t)lo8[1] << 16), (uint32_t)(lo8[2] & 0xFFFF) | ((uint32_t)lo8[3] << 16),
+              (uint32_t)(lo8[4] & 0xFFFF) | ((uint32_t)lo8[5] << 16), (uint32_t)(lo8[6] & 0xFFFF) | ((uint32_t)lo8[7] << 16));
+          *(uint4*)(op + 32) = make_uint4(
+              (uint32_t)(hi8[0] & 0xFFFF) | ((uint32_t)hi8[1] << 16), (uint32_t)(hi8[2] & 0xFFFF) | ((uint32_t)hi8[3] << 16),
+              (uint32_t)(hi8[4] & 0xFFFF) | ((uint32_t)hi8[5] << 16), (uint32_t)(hi8[6] & 0xFFFF) | ((uint32_t)hi8[7] << 16));
         }
       }
     }
@@ -180,9 +392,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
 
 template <int AW, int EPI>
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
-  constexpr int BM = AW == 2 ? 128 : 64, BN = 128, WM = AW == 2 ? 64 : 32, WN = 64;
-  dim3 grid((a.N + BN - 1) / BN, (a.M + BM - 1) / BM);
-  hipLaunchKernelGGL((gemm_kernel<AW, BM, BN, WM, WN, EPI>), grid, dim3(256), 0, s, a);
+  using C = GemmCfg<AW>;
+  const int nT = ((a.M + C::BM - 1) / C::BM) * ((a.N + C::BN - 1) / C::BN);
+  hipLaunchKernelGGL((gemm_kernel<AW, EPI>), dim3(8 * ((nT + 7) / 8)), dim3(512), 0, s, a);
   return hipGetLastError();
 }
 
@@ -270,8 +482,10 @@ __global__ __launch_bounds__(256) void silu_kernel(const int16_t* gu, int M, con
   const size_t t = (size_t)blockIdx.x * 256 + threadIdx.x;
   if (t >= (size_t)M * kDFF) return;
   const size_t row = t / kDFF, j = t % kDFF;
-  const int g = gu[row * (2 * kDFF) + j];
-  const int64_t u = gu[row * (2 * kDFF) + kDFF + j];
+  // gu rows hold [gate 32 | up 32] blocks: gate j at 64 (j / 32) + j % 32, up j 32 further
+  const size_t gi = row * (2 * kDFF) + 64 * (j / 32) + j % 32;
+  const int g = gu[gi];
+  const int64_t u = gu[gi + 32];
   const int64_t o = sat(rs((int64_t)silu[g + 32768] * u, sh), bits);
   if constexpr (OB == 2) ((int16_t*)gated)[t] = (int16_t)o;
   else ((int32_t*)gated)[t] = (int32_t)o;
@@ -489,24 +703,20 @@ inline unsigned blocks_for(size_t n) { return (unsigned)((n + 255) / 256); }
 }  // namespace
 
 hipError_t gemm(const GemmArgs& a, int a_bytes, int epi, hipStream_t s) {
-  if (a.K % kBK != 0 || a.M <= 0 || a.N <= 0) return hipErrorInvalidValue;
-  if (a_bytes == 2) {
-    switch (epi) {
-      case EPI_I64: return launch_gemm<2, EPI_I64>(a, s);
-      case EPI_REQ16: return launch_gemm<2, EPI_REQ16>(a, s);
-      case EPI_REQ32: return launch_gemm<2, EPI_REQ32>(a, s);
-      case EPI_RESID: return launch_gemm<2, EPI_RESID>(a, s);
-      case EPI_LOGITS: return launch_gemm<2, EPI_LOGITS>(a, s);
-    }
-  } else if (a_bytes == 4) {
-    switch (epi) {
-      case EPI_I64: return launch_gemm<4, EPI_I64>(a, s);
-      case EPI_REQ16: return launch_gemm<4, EPI_REQ16>(a, s);
-      case EPI_REQ32: return launch_gemm<4, EPI_REQ32>(a, s);
-      case EPI_RESID: return launch_gemm<4, EPI_RESID>(a, s);
-      case EPI_LOGITS: return launch_gemm<4, EPI_LOGITS>(a, s);
-    }
+  if (a.K % kBK != 0 || a.M <= 0 || a.N <= 0 || a.N % 4 != 0) return hipErrorInvalidValue;
+#define EII_EPIS(AW)                                                     \
+  switch (epi) {                                                         \
+    case EPI_I64: return launch_gemm<AW, EPI_I64>(a, s);                 \
+    case EPI_REQ16: return launch_gemm<AW, EPI_REQ16>(a, s);             \
+    case EPI_REQ32: return launch_gemm<AW, EPI_REQ32>(a, s);             \
+    case EPI_RESID: return launch_gemm<AW, EPI_RESID>(a, s);             \
+    case EPI_LOGITS: return launch_gemm<AW, EPI_LOGITS>(a, s);           \
+    case EPI_SILU: return launch_gemm<AW, EPI_SILU>(a, s);               \
+    case EPI_QKV: return launch_gemm<AW, EPI_QKV>(a, s);                 \
   }
+  if (a_bytes == 2) { EII_EPIS(2) }
+  else if (a_bytes == 4) { EII_EPIS(4) }
+#undef EII_EPIS
   return hipErrorInvalidValue;
 }
 

@@ -119,3 +119,36 @@ def test_attention_saturated(oracle):
 
 def test_attention_ctx32(oracle):
     _attention_case(oracle, [100], scale=3000.0, seed=5, f_c=27, bits_c=32)
+
+
+@pytest.mark.parametrize("a_bits,out_bits,M,N,K", [(16, 16, 300, 192, 576), (16, 32, 37, 576, 576),
+                                                    (32, 16, 130, 576, 1536), (32, 32, 64, 1536, 576),
+                                                    (16, 16, 257, 3072, 576)])
+def test_linear_requant(oracle, a_bits, out_bits, M, N, K):
+    # python/intref.py:186-190 on random operands, including the extreme activation values and
+    # multipliers at both ends of [2^13, 2^14]; shifts near their smallest and largest values
+    lib = L.load()
+    rng = np.random.default_rng(a_bits * 7 + out_bits + M)
+    lim = 2 ** (a_bits - 1)
+    a = rng.integers(-lim, lim, size=(M, K), dtype=np.int64)
+    a[0, :] = -lim
+    a[1, :] = lim - 1
+    a[2, :] = rng.integers(-3, 4, size=K)
+    W = rng.integers(-127, 128, size=(N, K), dtype=np.int8)
+    W[:, 0] = 127
+    m = rng.integers(2 ** 13, 2 ** 14 + 1, size=N, dtype=np.int64)
+    m[:2] = [2 ** 13, 2 ** 14]
+    n = rng.integers(18, 30, size=N, dtype=np.int64)
+    n[2:6] = [10, 11, 44, 45]
+    f_in, f_out = 12, 9
+    want, _ = oracle.linear(a, lim, (W, m, n), f_in, f_out, out_bits)
+    at = dev(a.astype(np.int16 if a_bits == 16 else np.int32))
+    wt = dev(W)
+    ws = torch.empty(N, dtype=torch.int32, device="cuda")
+    mt = dev(m.astype(np.int32))
+    st = dev((n + f_in - f_out).astype(np.int32))
+    out = torch.empty((M, N), dtype=torch.int16 if out_bits == 16 else torch.int32, device="cuda")
+    L.check(lib.eii_weight_colsum(p(wt), N, K, p(ws), None))
+    L.check(lib.eii_linear(p(at), a_bits, p(wt), p(ws), p(mt), p(st), M, N, K, out_bits, p(out), None))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(out.cpu().numpy().astype(np.int64), want)

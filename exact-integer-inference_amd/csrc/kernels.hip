@@ -39,8 +39,9 @@ __device__ __forceinline__ uint32_t byte_plane32(uint4 d, int i) {
 }
 
 // ------------------------------------------------------------------------------ GEMM
-// Workgroup = 8 waves over a BM x 128 output tile (BM = 256 for 2-limb activations, 128 for
-// 4-limb), K step 64, two LDS stages fed through registers.  The MFMA runs with the weights as
+// Workgroup = 4 waves over a BM x 128 output tile (BM = 128 for 2-limb activations, 64 for
+// 4-limb), K step 64, two LDS stages fed through registers; 61 KB of LDS lets two workgroups
+// share a CU, so one's epilogue overlaps the other's MFMA loop.  The MFMA runs with the weights as
 // the A operand and the activations as the B operand, D[n][m] = sum_k W[n,k] a[m,k]: a lane
 // then holds four output columns n = 4*(lane/16)+r of one row m = lane%16 per 16x16 tile.  The
 // order of the weight rows inside a wave's 64-column block is free, so it is chosen per
@@ -88,14 +89,16 @@ __device__ __forceinline__ int col_perm(int t, int g, int r) {
 
 template <int AW>
 struct GemmCfg {
-  static constexpr int BM = AW == 2 ? 256 : 128, BN = 128;
-  static constexpr int kWavesN = 2, WM = BM / 4, WN = 64;
+  static constexpr int kThreads = 256;                   // 4 waves; two workgroups share a CU
+  static constexpr int BM = AW == 2 ? 128 : 64, BN = 128;
+  static constexpr int kWavesN = 2, WM = BM / 2, WN = 64;
   static constexpr int TM = WM / 16, TN = 4;
   static constexpr int kPlane = BM * kLdsRow;
   static constexpr int kABytes = AW * kPlane;
   static constexpr int kStage = kABytes + BN * kLdsRow;
-  static constexpr int kAChunks = BM * 4 * AW / 512;   // 16-byte global loads per thread
-  static_assert(kAChunks * 512 == BM * 4 * AW, "A chunk split");
+  static constexpr int kAChunks = BM * 4 * AW / kThreads;   // 16-byte global loads per thread
+  static constexpr int kBChunks = BN * 4 / kThreads;
+  static_assert(kAChunks * kThreads == BM * 4 * AW && kBChunks * kThreads == BN * 4, "chunk split");
 };
 
 template <int EPI> struct EpiPerm { static constexpr int P = (EPI == EPI_SILU || EPI == EPI_QKV) ? PERM_PAIR : PERM_CONTIG; };
@@ -115,7 +118,7 @@ __device__ __forceinline__ bool tile_of(int nMB, int nNB, int& mb, int& nb) {
 }
 
 template <int AW, int EPI>
-__global__ __launch_bounds__(512) void gemm_kernel(GemmArgs g) {
+__global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
   using C = GemmCfg<AW>;
   constexpr int P = EpiPerm<EPI>::P;
   __shared__ __attribute__((aligned(16))) uint8_t smem[2 * C::kStage];
@@ -128,26 +131,32 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmArgs g) {
   const int nk = g.K / kBK;
   const uint8_t* Ab = (const uint8_t*)g.A;
 
-  // this thread's weight row (permuted within its 64-row block) and 16-byte chunk
-  const int wj = tid >> 2, wc = tid & 3;
-  const int wrow = n0 + (wj & 64) + col_perm<P>((wj & 63) >> 4, (wj & 15) >> 2, wj & 3);
-  const int8_t* wsrc = wrow < g.N ? g.W + (size_t)wrow * g.K + wc * 16 : nullptr;
+  // this thread's weight rows (permuted within their 64-row blocks) and 16-byte chunk
+  const int8_t* wsrc[C::kBChunks];
+#pragma unroll
+  for (int i = 0; i < C::kBChunks; ++i) {
+    const int wj = (tid + C::kThreads * i) >> 2, wc = tid & 3;
+    const int wrow = n0 + (wj & 64) + col_perm<P>((wj & 63) >> 4, (wj & 15) >> 2, wj & 3);
+    wsrc[i] = wrow < g.N ? g.W + (size_t)wrow * g.K + wc * 16 : nullptr;
+  }
 
-  uint4 areg[C::kAChunks], breg;
+  uint4 areg[C::kAChunks], breg[C::kBChunks];
   auto load = [&](int kb) {
 #pragma unroll
     for (int i = 0; i < C::kAChunks; ++i) {
-      const int q = tid + 512 * i, row = q / (4 * AW), c = q % (4 * AW), m = m0 + row;
+      const int q = tid + C::kThreads * i, row = q / (4 * AW), c = q % (4 * AW), m = m0 + row;
       areg[i] = m < g.M ? *(const uint4*)(Ab + ((size_t)m * g.K + (size_t)kb * kBK) * AW + c * 16)
                         : make_uint4(0, 0, 0, 0);
     }
-    breg = wsrc ? *(const uint4*)(wsrc + (size_t)kb * kBK) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < C::kBChunks; ++i)
+      breg[i] = wsrc[i] ? *(const uint4*)(wsrc[i] + (size_t)kb * kBK) : make_uint4(0, 0, 0, 0);
   };
   auto store = [&](int st) {
     uint8_t* base = smem + st * C::kStage;
 #pragma unroll
     for (int i = 0; i < C::kAChunks; ++i) {
-      const int q = tid + 512 * i, row = q / (4 * AW), c = q % (4 * AW);
+      const int q = tid + C::kThreads * i, row = q / (4 * AW), c = q % (4 * AW);
       const uint4 d = areg[i];
       if constexpr (AW == 2) {
         uint8_t* p = base + row * kLdsRow + c * 8;
@@ -159,7 +168,9 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmArgs g) {
         for (int pl = 0; pl < 4; ++pl) *(uint32_t*)(p + pl * C::kPlane) = byte_plane32(d, pl);
       }
     }
-    *(uint4*)(base + C::kABytes + wj * kLdsRow + wc * 16) = breg;
+#pragma unroll
+    for (int i = 0; i < C::kBChunks; ++i)
+      *(uint4*)(base + C::kABytes + ((tid + C::kThreads * i) >> 2) * kLdsRow + (tid & 3) * 16) = breg[i];
   };
 
   v4i acc[C::TM][C::TN][AW];
@@ -309,9 +320,9 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmArgs g) {
     // PERM_PAIR: lane holds block-local rows j = 8 gq + 4 (t & 1) + r (t = 0, 1) paired with j + 32
     // (t = 2, 3): (gate j, up j) for EPI_SILU, (d, d + 32) of one head for EPI_QKV.
     const int64_t bias = limb_bias(AW);
-    auto value16 = [&](int tm, int t, int r, int n) -> int32_t {   // SAT16(RS(acc * m, sh)) of column n
+    // SAT16(RS(acc * m, sh)) of the lane's value (tm, t, r) in column n, whose coefficients are k
+    auto value16 = [&](int tm, int t, int r, int n, const ColC& k) -> int32_t {
       if constexpr (AW == 2) {
-        const ColC k = col_coef(g.mult[n], g.shift[n], g.wsum[n]);
         return rne_i32(fmin(fmax(req2(acc[tm][t][1][r], acc[tm][t][0][r], k), -32768.0), 32767.0));
       } else {
         int64_t a = bias * (int64_t)g.wsum[n];
@@ -320,26 +331,35 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmArgs g) {
         return (int32_t)clamp_bits16(rs(a * g.mult[n], g.shift[n]));
       }
     };
+    auto coef = [&](int n) -> ColC {
+      if constexpr (AW == 2) return col_coef(g.mult[n], g.shift[n], g.wsum[n]);
+      else return ColC{0.0, 0.0, 0.0};
+    };
     if constexpr (EPI == EPI_SILU) {
       // gated[m, j]: j = 32 * (nblk / 64) + 8 gq + 4 t + r, t = 0, 1; weight rows nblk + j' and nblk + 32 + j'
       const int jb = (nblk >> 6) * 32 + 8 * gq;
       const double lo = -ldexp(1.0, g.bits2 - 1), hi = ldexp(1.0, g.bits2 - 1) - 1.0;
       if (nblk < g.N) {
+        int32_t vv[C::TM][8];
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int jl = 8 * gq + 4 * t + r;
+            const ColC kg = coef(nblk + jl), ku = coef(nblk + 32 + jl);
+#pragma unroll
+            for (int tm = 0; tm < C::TM; ++tm) {
+              const int32_t gv = value16(tm, t, r, nblk + jl, kg);
+              const int32_t uv = value16(tm, t + 2, r, nblk + 32 + jl, ku);
+              const double sg = (double)g.aux_tab[gv + 32768];
+              vv[tm][4 * t + r] = rs_sat_f64(sg * (double)uv, g.sh2, lo, hi);
+            }
+          }
 #pragma unroll
         for (int tm = 0; tm < C::TM; ++tm) {
           const int m = mrow[tm];
           if (m >= g.M) continue;
-          int32_t v[8];
-#pragma unroll
-          for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const int jl = 8 * gq + 4 * t + r;
-              const int32_t gv = value16(tm, t, r, nblk + jl);
-              const int32_t uv = value16(tm, t + 2, r, nblk + 32 + jl);
-              const double sg = (double)g.aux_tab[gv + 32768];
-              v[4 * t + r] = rs_sat_f64(sg * (double)uv, g.sh2, lo, hi);
-            }
+          const int32_t* v = vv[tm];
           const size_t o = (size_t)m * (g.N / 2) + jb;
           if (g.bits2 == 16) {
             *(uint4*)((int16_t*)g.out + o) = make_uint4(
@@ -355,6 +375,19 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmArgs g) {
       const int head = nblk >> 6;
       if (nblk < g.N) {
         const int shr = head < 9 ? g.sh_q : g.sh_k;
+        int32_t a1v[C::TM][8], a2v[C::TM][8];
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int d = 8 * gq + 4 * t + r;
+            const ColC k1 = coef(nblk + d), k2 = coef(nblk + 32 + d);
+#pragma unroll
+            for (int tm = 0; tm < C::TM; ++tm) {
+              a1v[tm][4 * t + r] = value16(tm, t, r, nblk + d, k1);
+              a2v[tm][4 * t + r] = value16(tm, t + 2, r, nblk + 32 + d, k2);
+            }
+          }
 #pragma unroll
         for (int tm = 0; tm < C::TM; ++tm) {
           const int m = mrow[tm];
@@ -366,7 +399,7 @@ __global__ __launch_bounds__(512) void gemm_kernel(GemmArgs g) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               const int d = 8 * gq + 4 * t + r;
-              const int32_t a1 = value16(tm, t, r, nblk + d), a2 = value16(tm, t + 2, r, nblk + 32 + d);
+              const int32_t a1 = a1v[tm][4 * t + r], a2 = a2v[tm][4 * t + r];
               if (head < 12) {
                 const double c = (double)g.cosT[ps * 32 + d], s = (double)g.sinT[ps * 32 + d];
                 const double o1 = fma((double)a1, c, -(double)a2 * s), o2 = fma((double)a2, c, (double)a1 * s);
@@ -394,7 +427,7 @@ template <int AW, int EPI>
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
   using C = GemmCfg<AW>;
   const int nT = ((a.M + C::BM - 1) / C::BM) * ((a.N + C::BN - 1) / C::BN);
-  hipLaunchKernelGGL((gemm_kernel<AW, EPI>), dim3(8 * ((nT + 7) / 8)), dim3(512), 0, s, a);
+  hipLaunchKernelGGL((gemm_kernel<AW, EPI>), dim3(8 * ((nT + 7) / 8)), dim3(C::kThreads), 0, s, a);
   return hipGetLastError();
 }
 

@@ -46,6 +46,7 @@ struct Mat {            // device arrays of one projection (possibly several mat
   int32_t* shift = nullptr;
   int32_t* wsum = nullptr;
   int N = 0, K = 0;
+  double2* coef = nullptr;   // [N] float64 requantization coefficients for 2-limb inputs
 };
 
 struct Layer {
@@ -215,7 +216,7 @@ extern "C" int eii_model_load(const char* path, int device, eii_model** out) {
   M->device = device;
 
   // offsets into the arena, resolved to device pointers after the upload
-  struct MatOff { size_t W, mult, shift, wsum; int N, K; };
+  struct MatOff { size_t W, mult, shift, wsum; int N, K; size_t coef; };
   size_t o_embq = ar.take((size_t)kV * kD);
   memcpy(ar.host.data() + o_embq, rd.bytes((size_t)kV * kD), (size_t)kV * kD);
   const std::vector<int64_t> emb_m = rd.vec(kV), emb_n = rd.vec(kV), fgq = rd.vec(kD);
@@ -227,6 +228,7 @@ extern "C" int eii_model_load(const char* path, int device, eii_model** out) {
   M->f_y = (int)f_y;
 
   size_t o_embm = ar.take(4 * kV), o_embsh = ar.take(4 * kV), o_headsh = ar.take(4 * kV), o_headws = ar.take(4 * kV);
+  size_t o_headcoef = ar.take(16 * (size_t)kV);
   size_t o_fg = ar.take(4 * kD), o_exp = ar.take(4 * (kDMax + 1)), o_rc = ar.take(4 * 512 * 32), o_rs = ar.take(4 * 512 * 32);
   {
     std::vector<int64_t> esh(kV), hsh(kV);
@@ -296,10 +298,12 @@ extern "C" int eii_model_load(const char* path, int device, eii_model** out) {
       return rc;
     }
     // projections, stacked: qkv = q | k | v, gu = gate | up
-    O.qkv = {ar.take((size_t)960 * 576), ar.take(4 * 960), ar.take(4 * 960), ar.take(4 * 960), 960, 576};
-    O.o = {ar.take((size_t)576 * 576), ar.take(4 * 576), ar.take(4 * 576), ar.take(4 * 576), 576, 576};
-    O.gu = {ar.take((size_t)3072 * 576), ar.take(4 * 3072), ar.take(4 * 3072), ar.take(4 * 3072), 3072, 576};
-    O.down = {ar.take((size_t)576 * 1536), ar.take(4 * 576), ar.take(4 * 576), ar.take(4 * 576), 576, 1536};
+    O.qkv = {ar.take((size_t)960 * 576), ar.take(4 * 960), ar.take(4 * 960), ar.take(4 * 960), 960, 576, ar.take(16 * 960)};
+    O.o = {ar.take((size_t)576 * 576), ar.take(4 * 576), ar.take(4 * 576), ar.take(4 * 576), 576, 576, ar.take(16 * 576)};
+    O.gu = {ar.take((size_t)3072 * 576), ar.take(4 * 3072), ar.take(4 * 3072), ar.take(4 * 3072), 3072, 576,
+            ar.take(16 * 3072)};
+    O.down = {ar.take((size_t)576 * 1536), ar.take(4 * 576), ar.take(4 * 576), ar.take(4 * 576), 576, 1536,
+              ar.take(16 * 576)};
     // matrix i -> (stack, row offset, f_in, f_out)
     const MatOff* dst[7] = {&O.qkv, &O.qkv, &O.qkv, &O.o, &O.gu, &O.gu, &O.down};
     const int row0[7] = {0, 576, 768, 0, 0, 32, 0};
@@ -352,14 +356,16 @@ extern "C" int eii_model_load(const char* path, int device, eii_model** out) {
   M->emb_q = (int8_t*)(d + o_embq);
   M->emb_m = (int32_t*)(d + o_embm);
   M->emb_sh = (int32_t*)(d + o_embsh);
-  M->head = {M->emb_q, M->emb_m, (int32_t*)(d + o_headsh), (int32_t*)(d + o_headws), kV, kD};
+  M->head = {M->emb_q, M->emb_m, (int32_t*)(d + o_headsh), (int32_t*)(d + o_headws), kV, kD,
+             (double2*)(d + o_headcoef)};
   M->fg = (int32_t*)(d + o_fg);
   M->exp_tab = (int32_t*)(d + o_exp);
   M->rope_c = (int32_t*)(d + o_rc);
   M->rope_s = (int32_t*)(d + o_rs);
   M->rope_rows = 512;
   auto mat = [&](const MatOff& o) {
-    return Mat{(int8_t*)(d + o.W), (int32_t*)(d + o.mult), (int32_t*)(d + o.shift), (int32_t*)(d + o.wsum), o.N, o.K};
+    return Mat{(int8_t*)(d + o.W), (int32_t*)(d + o.mult), (int32_t*)(d + o.shift), (int32_t*)(d + o.wsum), o.N, o.K,
+               (double2*)(d + o.coef)};
   };
   for (int l = 0; l < kNL; ++l) {
     Layer& L = M->L[l];
@@ -373,11 +379,16 @@ extern "C" int eii_model_load(const char* path, int device, eii_model** out) {
   }
   M->fy_raw = f_y;
   // weight row sums for the limb bias correction
+  // weight row sums for the limb bias correction, then the float64 requantization coefficients
   hipError_t e = weight_colsum(M->head.W, kV, kD, M->head.wsum, nullptr);
+  if (e == hipSuccess) e = gemm_coef(M->head.mult, M->head.shift, M->head.wsum, kV, M->head.coef, nullptr);
   for (int l = 0; l < kNL && e == hipSuccess; ++l) {
     Layer& L = M->L[l];
     Mat* ms[4] = {&L.qkv, &L.o, &L.gu, &L.down};
-    for (Mat* m : ms) if (e == hipSuccess) e = weight_colsum(m->W, m->N, m->K, m->wsum, nullptr);
+    for (Mat* m : ms) {
+      if (e == hipSuccess) e = weight_colsum(m->W, m->N, m->K, m->wsum, nullptr);
+      if (e == hipSuccess) e = gemm_coef(m->mult, m->shift, m->wsum, m->N, m->coef, nullptr);
+    }
   }
   if (e == hipSuccess) e = hipMalloc(&M->flags, 16);
   if (e == hipSuccess) e = hipMemset(M->flags, 0, 16);
@@ -488,12 +499,14 @@ int set_batch(eii_model* m, const std::vector<int32_t>& lens, hipStream_t s) {
 
 int gemm_req(const Mat& W, const void* A, int a_bytes, int M, void* out, int out_bits, hipStream_t s) {
   GemmArgs g{A, W.W, M, W.N, W.K, W.wsum, W.mult, W.shift, out, out_bits, nullptr};
+  g.coef = W.coef;
   HIPCHK(gemm(g, a_bytes, out_bits == 16 ? EPI_REQ16 : EPI_REQ32, s));
   return EII_OK;
 }
 
 int gemm_resid(const Mat& W, const void* A, int a_bytes, int M, int32_t* x, hipStream_t s) {
   GemmArgs g{A, W.W, M, W.N, W.K, W.wsum, W.mult, W.shift, x, 32, nullptr};
+  g.coef = W.coef;
   HIPCHK(gemm(g, a_bytes, EPI_RESID, s));
   return EII_OK;
 }
@@ -518,7 +531,7 @@ int run_block(eii_model* m, int l, int32_t* x, int M, int nseq, int max_T, const
     // q, k, v projections with RoPE applied in the epilogue
     ProfScope ps(m, EII_K_GEMM_QKV, s);
     GemmArgs g{m->h, L.qkv.W, M, L.qkv.N, L.qkv.K, L.qkv.wsum, L.qkv.mult, L.qkv.shift, m->qkv, 16, nullptr};
-    g.pos = m->pos; g.cosT = m->rope_c; g.sinT = m->rope_s; g.sh_q = sh_q; g.sh_k = sh_k;
+    g.pos = m->pos; g.cosT = m->rope_c; g.sinT = m->rope_s; g.sh_q = sh_q; g.sh_k = sh_k; g.coef = L.qkv.coef;
     HIPCHK(gemm(g, hb, EPI_QKV, s));
   } else {
     if ((rc = gemm_req(L.qkv, m->h, hb, M, m->qkv, 16, s))) return rc;
@@ -554,7 +567,7 @@ int run_block(eii_model* m, int l, int32_t* x, int M, int nseq, int max_T, const
     // gate and up projections with the SiLU table and the gated product in the epilogue
     ProfScope ps(m, EII_K_GEMM_GU, s);
     GemmArgs g{m->h, L.gu.W, M, L.gu.N, L.gu.K, L.gu.wsum, L.gu.mult, L.gu.shift, m->gated, 16, nullptr};
-    g.aux_tab = L.silu; g.sh2 = sh_s; g.bits2 = L.bits[GATED];
+    g.aux_tab = L.silu; g.sh2 = sh_s; g.bits2 = L.bits[GATED]; g.coef = L.gu.coef;
     HIPCHK(gemm(g, h2b, EPI_SILU, s));
   } else {
     if ((rc = gemm_req(L.gu, m->h, h2b, M, m->gu, 16, s))) return rc;
@@ -580,6 +593,7 @@ int run_final(eii_model* m, const int32_t* x, int M, int32_t* logits, hipStream_
     HIPCHK(rmsnorm(x, M, m->fg, 21 + m->fg_f - m->f_y, 16, m->h, 2, s));
   }
   GemmArgs g{m->h, m->head.W, M, kV, kD, m->head.wsum, m->head.mult, m->head.shift, logits, 32, m->flags};
+  g.coef = m->head.coef;
   ProfScope ps(m, EII_K_GEMM_HEAD, s);
   HIPCHK(gemm(g, 2, EPI_LOGITS, s));
   return EII_OK;
@@ -749,8 +763,18 @@ extern "C" int eii_linear(const void* A, int a_bits, const int8_t* W, const int3
   if ((rc = check_gemm_args(A, a_bits, W, M, N, K))) return rc;
   if (!wsum || !mult || !shift || !out) return fail(EII_E_ARG, "null argument");
   if (out_bits != 16 && out_bits != 32) return fail(EII_E_ARG, "out_bits must be 16 or 32");
+  hipStream_t s = (hipStream_t)stream;
   GemmArgs g{A, W, M, N, K, wsum, mult, shift, out, out_bits, nullptr};
-  HIPCHK(gemm(g, a_bits / 8, out_bits == 16 ? EPI_REQ16 : EPI_REQ32, (hipStream_t)stream));
+  double2* coef = nullptr;
+  if (a_bits == 16) {
+    HIPCHK(hipMallocAsync((void**)&coef, (size_t)N * sizeof(double2), s));
+    hipError_t e = gemm_coef(mult, shift, wsum, N, coef, s);
+    if (e != hipSuccess) { (void)hipFreeAsync(coef, s); return fail(EII_E_DEVICE, hipGetErrorString(e)); }
+    g.coef = coef;
+  }
+  hipError_t e = gemm(g, a_bits / 8, out_bits == 16 ? EPI_REQ16 : EPI_REQ32, s);
+  if (coef) (void)hipFreeAsync(coef, s);
+  if (e != hipSuccess) return fail(EII_E_DEVICE, std::string("eii_linear: ") + hipGetErrorString(e));
   return EII_OK;
 }
 

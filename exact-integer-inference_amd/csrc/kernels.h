@@ -30,6 +30,9 @@ struct GemmArgs {
   void* out;
   int sat_bits;
   int* flag;
+  // 2-limb inputs, every epilogue except EPI_I64: per-column float64 coefficients [N]
+  // (m 2^-sh, 128 wsum m 2^-sh + 2^-(sh+1)) from gemm_coef
+  const double2* coef = nullptr;
   // EPI_SILU
   const int32_t* aux_tab = nullptr;
   int sh2 = 0, bits2 = 16;
@@ -42,6 +45,8 @@ struct GemmArgs {
 
 hipError_t gemm(const GemmArgs& a, int a_bytes, int epi, hipStream_t s);
 hipError_t weight_colsum(const int8_t* W, int N, int K, int32_t* wsum, hipStream_t s);
+hipError_t gemm_coef(const int32_t* mult, const int32_t* shift, const int32_t* wsum, int N, double2* coef,
+                     hipStream_t s);
 
 // x[m, c] = RS(emb_q[id, c] * emb_m[id], emb_sh[id]) (python/intref.py:163-166)
 hipError_t embed(const int64_t* ids, int M, const int8_t* emb_q, const int32_t* emb_m,

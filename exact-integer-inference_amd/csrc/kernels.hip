@@ -7,6 +7,9 @@
 // The elementwise kernels are one pass over HBM each; attention computes QK and PV as
 // integer MFMA tiles with the reference's three-step exact softmax (row max, exp-table sum,
 // rounded Q0.16 division).
+#include <algorithm>
+#include <type_traits>
+
 #include "eii_int.h"
 #include "kernels.h"
 
@@ -61,17 +64,11 @@ __device__ __forceinline__ int32_t rne_i32(double y) {   // |y| < 2^31 after cla
   return (int32_t)(uint32_t)(uint64_t)__double_as_longlong(y + kMagic);
 }
 
-struct ColC { double c0, c1, cb; };
-__device__ __forceinline__ ColC col_coef(int32_t mu, int sh, int32_t ws) {
-  ColC k;
-  k.c0 = ldexp((double)mu, -sh);
-  k.c1 = k.c0 * 256.0;
-  k.cb = fma((double)ws * 128.0, k.c0, ldexp(0.5, -sh));   // per-column shifts are >= 1
-  return k;
-}
-// acc * m / 2^sh + 2^-(sh+1) for acc = 256 P1 + P0 + 128 wsum (exact, see above)
-__device__ __forceinline__ double req2(int32_t P1, int32_t P0, const ColC& k) {
-  return fma((double)P1, k.c1, fma((double)P0, k.c0, k.cb));
+// Per-column coefficients for 2-limb inputs, precomputed once per weight matrix (coef_kernel):
+//   c0 = m 2^-sh,  cb = 128 wsum m 2^-sh + 2^-(sh+1).
+// acc * m / 2^sh + 2^-(sh+1) for acc = 256 P1 + P0 + 128 wsum (exact, see above):
+__device__ __forceinline__ double req2(int32_t P1, int32_t P0, double2 k) {
+  return fma((double)P1 * 256.0, k.x, fma((double)P0, k.x, k.y));
 }
 // SAT(RS(x, sh), bits) for an integer-valued double x with |x| < 2^52 (scalar shift, any sign)
 __device__ __forceinline__ int32_t rs_sat_f64(double x, int sh, double lo, double hi) {
@@ -103,18 +100,15 @@ struct GemmCfg {
 
 template <int EPI> struct EpiPerm { static constexpr int P = (EPI == EPI_SILU || EPI == EPI_QKV) ? PERM_PAIR : PERM_CONTIG; };
 
-// Tile of a workgroup: XCD x (= blockIdx % 8, the hardware's round-robin) takes a contiguous
-// range of tiles in grouped order (8 row blocks x all column blocks), so concurrently running
-// workgroups of one XCD share activation rows and weight blocks in that XCD's L2.
-__device__ __forceinline__ bool tile_of(int nMB, int nNB, int& mb, int& nb) {
-  const int nT = nMB * nNB, per = (nT + 7) / 8;
-  const int v = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
-  if (v >= nT) return false;
+// Tiles in grouped order: 8 row blocks x all column blocks per group.  Each XCD (= blockIdx % 8,
+// the hardware's round-robin dispatch) owns a contiguous range of that order, and the persistent
+// workgroups of one XCD sweep it together, so concurrently running tiles of an XCD share
+// activation rows and weight blocks in its L2.
+__device__ __forceinline__ void tile_coords(int v, int nMB, int nNB, int& mb, int& nb) {
   const int G = 8, grp = v / (G * nNB), first = grp * G;
   const int gs = min(nMB - first, G), in = v - grp * G * nNB;
   mb = first + in % gs;
   nb = in / gs;
-  return true;
 }
 
 template <int AW, int EPI>
@@ -122,42 +116,46 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
   using C = GemmCfg<AW>;
   constexpr int P = EpiPerm<EPI>::P;
   __shared__ __attribute__((aligned(16))) uint8_t smem[2 * C::kStage];
-  int mb, nb;
-  if (!tile_of((g.M + C::BM - 1) / C::BM, (g.N + C::BN - 1) / C::BN, mb, nb)) return;
+  const int nMB = (g.M + C::BM - 1) / C::BM, nNB = (g.N + C::BN - 1) / C::BN, nT = nMB * nNB;
+  // this workgroup's tiles: v = v0, v0 + stride, ... < vend
+  const int xcd = blockIdx.x & 7, per = (nT + 7) / 8, nwg_x = gridDim.x >> 3;
+  const int v0 = xcd * per + (blockIdx.x >> 3), vend = min(nT, (xcd + 1) * per);
+  if (v0 >= vend) return;
+  const int ntiles = (vend - v0 + nwg_x - 1) / nwg_x;
+  const int nk = g.K / kBK, nsteps = ntiles * nk;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  const int m0 = mb * C::BM, n0 = nb * C::BN;
-  const int nk = g.K / kBK;
   const uint8_t* Ab = (const uint8_t*)g.A;
 
-  // this thread's weight rows (permuted within their 64-row blocks) and 16-byte chunk
-  const int8_t* wsrc[C::kBChunks];
-#pragma unroll
-  for (int i = 0; i < C::kBChunks; ++i) {
-    const int wj = (tid + C::kThreads * i) >> 2, wc = tid & 3;
-    const int wrow = n0 + (wj & 64) + col_perm<P>((wj & 63) >> 4, (wj & 15) >> 2, wj & 3);
-    wsrc[i] = wrow < g.N ? g.W + (size_t)wrow * g.K + wc * 16 : nullptr;
-  }
-
-  uint4 areg[C::kAChunks], breg[C::kBChunks];
-  auto load = [&](int kb) {
+  // global loads of step s (tile s / nk, k block s % nk) into register set rs
+  uint4 areg[2][C::kAChunks], breg[2][C::kBChunks];
+  auto load = [&](int st, int set) {
+    const int j = st / nk, kb = st - j * nk;
+    int mb, nb;
+    tile_coords(v0 + j * nwg_x, nMB, nNB, mb, nb);
+    const int m0 = mb * C::BM, n0 = nb * C::BN;
 #pragma unroll
     for (int i = 0; i < C::kAChunks; ++i) {
       const int q = tid + C::kThreads * i, row = q / (4 * AW), c = q % (4 * AW), m = m0 + row;
-      areg[i] = m < g.M ? *(const uint4*)(Ab + ((size_t)m * g.K + (size_t)kb * kBK) * AW + c * 16)
-                        : make_uint4(0, 0, 0, 0);
+      areg[set][i] = m < g.M ? *(const uint4*)(Ab + ((size_t)m * g.K + (size_t)kb * kBK) * AW + c * 16)
+                             : make_uint4(0, 0, 0, 0);
     }
 #pragma unroll
-    for (int i = 0; i < C::kBChunks; ++i)
-      breg[i] = wsrc[i] ? *(const uint4*)(wsrc[i] + (size_t)kb * kBK) : make_uint4(0, 0, 0, 0);
+    for (int i = 0; i < C::kBChunks; ++i) {
+      // weight rows permuted within their 64-row blocks (col_perm)
+      const int wj = (tid + C::kThreads * i) >> 2;
+      const int wrow = n0 + (wj & 64) + col_perm<P>((wj & 63) >> 4, (wj & 15) >> 2, wj & 3);
+      breg[set][i] = wrow < g.N ? *(const uint4*)(g.W + (size_t)wrow * g.K + (size_t)kb * kBK + (tid & 3) * 16)
+                                : make_uint4(0, 0, 0, 0);
+    }
   };
-  auto store = [&](int st) {
-    uint8_t* base = smem + st * C::kStage;
+  auto store = [&](int stage, int set) {
+    uint8_t* base = smem + stage * C::kStage;
 #pragma unroll
     for (int i = 0; i < C::kAChunks; ++i) {
       const int q = tid + C::kThreads * i, row = q / (4 * AW), c = q % (4 * AW);
-      const uint4 d = areg[i];
+      const uint4 d = areg[set][i];
       if constexpr (AW == 2) {
         uint8_t* p = base + row * kLdsRow + c * 8;
         *(uint2*)(p) = make_uint2(lo_bytes16(d.x, d.y), lo_bytes16(d.z, d.w));
@@ -170,7 +168,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
     }
 #pragma unroll
     for (int i = 0; i < C::kBChunks; ++i)
-      *(uint4*)(base + C::kABytes + ((tid + C::kThreads * i) >> 2) * kLdsRow + (tid & 3) * 16) = breg[i];
+      *(uint4*)(base + C::kABytes + ((tid + C::kThreads * i) >> 2) * kLdsRow + (tid & 3) * 16) = breg[set][i];
   };
 
   v4i acc[C::TM][C::TN][AW];
@@ -181,13 +179,17 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
 #pragma unroll
       for (int l = 0; l < AW; ++l) acc[a][b][l] = v4i{0, 0, 0, 0};
 
-  load(0);
-  store(0);
+  // Step s computes from LDS stage s % 2; its global data was loaded two steps earlier into
+  // register set s % 2 and stored to LDS during step s - 1.
+  load(0, 0);
+  if (nsteps > 1) load(1, 1);
+  store(0, 0);
   __syncthreads();
   const int fr = lane & 15, fk = (lane >> 4) * 16;
-  for (int kb = 0; kb < nk; ++kb) {
-    const int cur = kb & 1;
-    if (kb + 1 < nk) load(kb + 1);
+  // one step; CUR = st % 2 is a compile-time constant so the register sets stay in registers
+  auto step = [&](auto CUR, int st) {
+    constexpr int cur = decltype(CUR)::value;
+    if (st + 2 < nsteps) load(st + 2, cur);
     const uint8_t* base = smem + cur * C::kStage;
     v4i wf[C::TN];
 #pragma unroll
@@ -202,10 +204,14 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
         for (int tn = 0; tn < C::TN; ++tn) acc[tm][tn][l] = mfma(wf[tn], af, acc[tm][tn][l]);
       }
     }
-    if (kb + 1 < nk) store(cur ^ 1);
+    if (st + 1 < nsteps) store(cur ^ 1, cur ^ 1);
     __syncthreads();
-  }
+    const int j = st / nk;
+    if (st - j * nk != nk - 1) return;
 
+    int mb, nb;
+    tile_coords(v0 + j * nwg_x, nMB, nNB, mb, nb);
+    const int m0 = mb * C::BM, n0 = nb * C::BN;
   // ---------------------------------------------------------------- epilogue
   const int gq = lane >> 4;
   const int nblk = n0 + wn * C::WN;                     // first column of this wave's block
@@ -221,15 +227,15 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
     for (int t = 0; t < C::TN; ++t) {
       const int nc = nblk + 16 * gq + 4 * t;           // 4 consecutive columns nc..nc+3
       if (nc >= g.N) continue;                          // N is a multiple of 4
-      const int4 ws4 = *(const int4*)(g.wsum + nc);
-      int4 mu4 = make_int4(0, 0, 0, 0), sh4 = make_int4(1, 1, 1, 1);
-      if constexpr (EPI != EPI_I64) { mu4 = *(const int4*)(g.mult + nc); sh4 = *(const int4*)(g.shift + nc); }
+      int4 ws4 = make_int4(0, 0, 0, 0), mu4 = make_int4(0, 0, 0, 0), sh4 = make_int4(1, 1, 1, 1);
+      if constexpr (AW == 4 || EPI == EPI_I64) ws4 = *(const int4*)(g.wsum + nc);
+      if constexpr (AW == 4 && EPI != EPI_I64) { mu4 = *(const int4*)(g.mult + nc); sh4 = *(const int4*)(g.shift + nc); }
       const int wsv[4] = {ws4.x, ws4.y, ws4.z, ws4.w}, muv[4] = {mu4.x, mu4.y, mu4.z, mu4.w},
                 shv[4] = {sh4.x, sh4.y, sh4.z, sh4.w};
       if constexpr (AW == 2 && EPI != EPI_I64) {
-        ColC k[4];
+        double2 k[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) k[r] = col_coef(muv[r], shv[r], wsv[r]);
+        for (int r = 0; r < 4; ++r) k[r] = g.coef[nc + r];
 #pragma unroll
         for (int tm = 0; tm < C::TM; ++tm) {
           const int m = mrow[tm];
@@ -320,10 +326,10 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
     // PERM_PAIR: lane holds block-local rows j = 8 gq + 4 (t & 1) + r (t = 0, 1) paired with j + 32
     // (t = 2, 3): (gate j, up j) for EPI_SILU, (d, d + 32) of one head for EPI_QKV.
     const int64_t bias = limb_bias(AW);
-    // SAT16(RS(acc * m, sh)) of the lane's value (tm, t, r) in column n, whose coefficients are k
-    auto value16 = [&](int tm, int t, int r, int n, const ColC& k) -> int32_t {
+    // SAT16(RS(acc * m, sh)) of the lane's value (tm, t, r) in column n
+    auto value16 = [&](int tm, int t, int r, int n) -> int32_t {
       if constexpr (AW == 2) {
-        return rne_i32(fmin(fmax(req2(acc[tm][t][1][r], acc[tm][t][0][r], k), -32768.0), 32767.0));
+        return rne_i32(fmin(fmax(req2(acc[tm][t][1][r], acc[tm][t][0][r], g.coef[n]), -32768.0), 32767.0));
       } else {
         int64_t a = bias * (int64_t)g.wsum[n];
 #pragma unroll
@@ -331,35 +337,26 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
         return (int32_t)clamp_bits16(rs(a * g.mult[n], g.shift[n]));
       }
     };
-    auto coef = [&](int n) -> ColC {
-      if constexpr (AW == 2) return col_coef(g.mult[n], g.shift[n], g.wsum[n]);
-      else return ColC{0.0, 0.0, 0.0};
-    };
-    if constexpr (EPI == EPI_SILU) {
-      // gated[m, j]: j = 32 * (nblk / 64) + 8 gq + 4 t + r, t = 0, 1; weight rows nblk + j' and nblk + 32 + j'
-      const int jb = (nblk >> 6) * 32 + 8 * gq;
-      const double lo = -ldexp(1.0, g.bits2 - 1), hi = ldexp(1.0, g.bits2 - 1) - 1.0;
-      if (nblk < g.N) {
-        int32_t vv[C::TM][8];
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int jl = 8 * gq + 4 * t + r;
-            const ColC kg = coef(nblk + jl), ku = coef(nblk + 32 + jl);
-#pragma unroll
-            for (int tm = 0; tm < C::TM; ++tm) {
-              const int32_t gv = value16(tm, t, r, nblk + jl, kg);
-              const int32_t uv = value16(tm, t + 2, r, nblk + 32 + jl, ku);
-              const double sg = (double)g.aux_tab[gv + 32768];
-              vv[tm][4 * t + r] = rs_sat_f64(sg * (double)uv, g.sh2, lo, hi);
-            }
-          }
+    if (nblk < g.N) {
+      if constexpr (EPI == EPI_SILU) {
+        // gated[m, j]: j = 32 * (nblk / 64) + 8 gq + 4 t + r, t = 0, 1; weight rows nblk + j' and nblk + 32 + j'
+        const int jb = (nblk >> 6) * 32 + 8 * gq;
+        const double lo = -ldexp(1.0, g.bits2 - 1), hi = ldexp(1.0, g.bits2 - 1) - 1.0;
 #pragma unroll
         for (int tm = 0; tm < C::TM; ++tm) {
           const int m = mrow[tm];
           if (m >= g.M) continue;
-          const int32_t* v = vv[tm];
+          int32_t v[8];
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int jl = 8 * gq + 4 * t + r;
+              const int32_t gv = value16(tm, t, r, nblk + jl);
+              const int32_t uv = value16(tm, t + 2, r, nblk + 32 + jl);
+              const double sg = (double)g.aux_tab[gv + 32768];
+              v[4 * t + r] = rs_sat_f64(sg * (double)uv, g.sh2, lo, hi);
+            }
           const size_t o = (size_t)m * (g.N / 2) + jb;
           if (g.bits2 == 16) {
             *(uint4*)((int16_t*)g.out + o) = make_uint4(
@@ -370,24 +367,9 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
             *(int4*)((int32_t*)g.out + o + 4) = make_int4(v[4], v[5], v[6], v[7]);
           }
         }
-      }
-    } else {   // EPI_QKV: heads 0..8 q and 9..11 k get RoPE, 12..14 v are stored as they are
-      const int head = nblk >> 6;
-      if (nblk < g.N) {
+      } else {   // EPI_QKV: heads 0..8 q and 9..11 k get RoPE, 12..14 v are stored as they are
+        const int head = nblk >> 6;
         const int shr = head < 9 ? g.sh_q : g.sh_k;
-        int32_t a1v[C::TM][8], a2v[C::TM][8];
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int d = 8 * gq + 4 * t + r;
-            const ColC k1 = coef(nblk + d), k2 = coef(nblk + 32 + d);
-#pragma unroll
-            for (int tm = 0; tm < C::TM; ++tm) {
-              a1v[tm][4 * t + r] = value16(tm, t, r, nblk + d, k1);
-              a2v[tm][4 * t + r] = value16(tm, t + 2, r, nblk + 32 + d, k2);
-            }
-          }
 #pragma unroll
         for (int tm = 0; tm < C::TM; ++tm) {
           const int m = mrow[tm];
@@ -399,10 +381,10 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               const int d = 8 * gq + 4 * t + r;
-              const int32_t a1 = a1v[tm][4 * t + r], a2 = a2v[tm][4 * t + r];
+              const int32_t a1 = value16(tm, t, r, nblk + d), a2 = value16(tm, t + 2, r, nblk + 32 + d);
               if (head < 12) {
-                const double c = (double)g.cosT[ps * 32 + d], s = (double)g.sinT[ps * 32 + d];
-                const double o1 = fma((double)a1, c, -(double)a2 * s), o2 = fma((double)a2, c, (double)a1 * s);
+                const double c = (double)g.cosT[ps * 32 + d], sn = (double)g.sinT[ps * 32 + d];
+                const double o1 = fma((double)a1, c, -(double)a2 * sn), o2 = fma((double)a2, c, (double)a1 * sn);
                 lo8[4 * t + r] = rs_sat_f64(o1, shr, -32768.0, 32767.0);
                 hi8[4 * t + r] = rs_sat_f64(o2, shr, -32768.0, 32767.0);
               } else {
@@ -421,14 +403,47 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
       }
     }
   }
+#pragma unroll
+    for (int a = 0; a < C::TM; ++a)
+#pragma unroll
+      for (int b = 0; b < C::TN; ++b)
+#pragma unroll
+        for (int l = 0; l < AW; ++l) acc[a][b][l] = v4i{0, 0, 0, 0};
+  };
+  for (int st = 0; st < nsteps; st += 2) {
+    step(std::integral_constant<int, 0>{}, st);
+    if (st + 1 < nsteps) step(std::integral_constant<int, 1>{}, st + 1);
+  }
+}
+
+int device_cus() {
+  static int cus = 0;
+  if (!cus) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      cus = 256;
+  }
+  return cus;
 }
 
 template <int AW, int EPI>
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
   using C = GemmCfg<AW>;
   const int nT = ((a.M + C::BM - 1) / C::BM) * ((a.N + C::BN - 1) / C::BN);
-  hipLaunchKernelGGL((gemm_kernel<AW, EPI>), dim3(8 * ((nT + 7) / 8)), dim3(C::kThreads), 0, s, a);
+  // two persistent workgroups per CU, a multiple of 8 so every XCD gets the same count
+  const int per_xcd = std::min((nT + 7) / 8, std::max(1, 2 * device_cus() / 8));
+  hipLaunchKernelGGL((gemm_kernel<AW, EPI>), dim3(8 * per_xcd), dim3(C::kThreads), 0, s, a);
   return hipGetLastError();
+}
+
+__global__ __launch_bounds__(256) void coef_kernel(const int32_t* mult, const int32_t* shift, const int32_t* wsum,
+                                                   int N, double2* coef) {
+  const int n = blockIdx.x * 256 + threadIdx.x;
+  if (n >= N) return;
+  const int sh = shift[n];
+  const double c0 = ldexp((double)mult[n], -sh);
+  coef[n] = make_double2(c0, fma((double)wsum[n] * 128.0, c0, ldexp(0.5, -sh)));
 }
 
 __global__ __launch_bounds__(256) void colsum_kernel(const int8_t* W, int N, int K, int32_t* wsum) {
@@ -737,6 +752,7 @@ inline unsigned blocks_for(size_t n) { return (unsigned)((n + 255) / 256); }
 
 hipError_t gemm(const GemmArgs& a, int a_bytes, int epi, hipStream_t s) {
   if (a.K % kBK != 0 || a.M <= 0 || a.N <= 0 || a.N % 4 != 0) return hipErrorInvalidValue;
+  if (a_bytes == 2 && epi != EPI_I64 && !a.coef) return hipErrorInvalidValue;
 #define EII_EPIS(AW)                                                     \
   switch (epi) {                                                         \
     case EPI_I64: return launch_gemm<AW, EPI_I64>(a, s);                 \
@@ -751,6 +767,12 @@ hipError_t gemm(const GemmArgs& a, int a_bytes, int epi, hipStream_t s) {
   else if (a_bytes == 4) { EII_EPIS(4) }
 #undef EII_EPIS
   return hipErrorInvalidValue;
+}
+
+hipError_t gemm_coef(const int32_t* mult, const int32_t* shift, const int32_t* wsum, int N, double2* coef,
+                     hipStream_t s) {
+  hipLaunchKernelGGL(coef_kernel, dim3((N + 255) / 256), dim3(256), 0, s, mult, shift, wsum, N, coef);
+  return hipGetLastError();
 }
 
 hipError_t weight_colsum(const int8_t* W, int N, int K, int32_t* wsum, hipStream_t s) {

@@ -42,14 +42,14 @@ __device__ __forceinline__ uint32_t byte_plane32(uint4 d, int i) {
 }
 
 // ------------------------------------------------------------------------------ GEMM
-// Workgroup = 4 waves over a BM x 128 output tile (BM = 128 for 2-limb activations, 64 for
-// 4-limb), K step 64, two LDS stages fed through registers; 61 KB of LDS lets two workgroups
-// share a CU, so one's epilogue overlaps the other's MFMA loop.  The MFMA runs with the weights as
-// the A operand and the activations as the B operand, D[n][m] = sum_k W[n,k] a[m,k]: a lane
-// then holds four output columns n = 4*(lane/16)+r of one row m = lane%16 per 16x16 tile.  The
-// order of the weight rows inside a wave's 64-column block is free, so it is chosen per
-// epilogue (col_perm) to give each lane 16 consecutive columns (contiguous stores), or the
-// (gate j, up j) and RoPE (d, d+32) pairs in one lane.
+// Persistent workgroups of 4 waves (two per CU, so one's epilogue overlaps the other's MFMA loop)
+// sweep BM x 128 output tiles (BM = 128 for 2-limb activations, 64 for 4-limb) in a flat
+// (tile, K block of 64) loop with two LDS stages fed through registers loaded two steps ahead.
+// v_mfma_i32_32x32x32_i8 runs with the weights as the A operand and the activations as the B
+// operand, D[n][m] = sum_k W[n,k] a[m,k]; it sustains about twice the int8 rate of the 16x16x64
+// form on gfx950.  The order of the weight rows inside a wave's 64-column block is free, so it is
+// chosen per epilogue (col_perm): 32 consecutive output columns per lane (contiguous stores), or
+// the (gate j, up j) and RoPE (d, d+32) pairs in one lane.
 //
 // Epilogue arithmetic for 2-limb inputs runs in float64 and is exact: with P1, P0 the limb
 // partial sums (|P| < 2^25 for K <= 1536) and |m| <= 2^14,
@@ -77,19 +77,31 @@ __device__ __forceinline__ int32_t rs_sat_f64(double x, int sh, double lo, doubl
 }
 
 enum Perm { PERM_CONTIG = 0, PERM_PAIR = 1 };
-// Row of a wave's 64-column weight block held at (n-tile t, lane group g, register r).
+
+typedef int v16i __attribute__((ext_vector_type(16)));
+__device__ __forceinline__ v16i mfma32(v4i a, v4i b, v16i c) {
+  return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+}
+
+// 32x32 output tile of v_mfma_i32_32x32x32_i8, lane = 32 h + c, register j = 4 b + r: row
+// i = 8 b + 4 h + r, column c.  The weights are the A operand, so i indexes a weight row of the
+// tile.  Column of a wave's 64-column block held at (n-tile tn, tile row i):
+//   PERM_CONTIG: lane h holds block columns 32h .. 32h+31 (contiguous stores)
+//   PERM_PAIR:   lane h holds 16h .. 16h+15 (tn = 0) and 32+16h .. 32+16h+15 (tn = 1), i.e. the
+//                (gate j, up j) and RoPE (d, d + 32) pairs
 template <int P>
-__device__ __forceinline__ int col_perm(int t, int g, int r) {
-  if constexpr (P == PERM_CONTIG) return 16 * g + 4 * t + r;           // lane g: columns 16g..16g+15
-  else return 32 * (t >> 1) + 8 * g + 4 * (t & 1) + r;                 // lane g: 8g..8g+7 and 32+8g..
+__device__ __forceinline__ int col_perm(int tn, int i) {
+  const int b = i >> 3, h = (i >> 2) & 1, r = i & 3;
+  if constexpr (P == PERM_CONTIG) return 32 * h + 16 * tn + 4 * b + r;
+  else return 32 * tn + 16 * h + 4 * b + r;
 }
 
 template <int AW>
 struct GemmCfg {
   static constexpr int kThreads = 256;                   // 4 waves; two workgroups share a CU
   static constexpr int BM = AW == 2 ? 128 : 64, BN = 128;
-  static constexpr int kWavesN = 2, WM = BM / 2, WN = 64;
-  static constexpr int TM = WM / 16, TN = 4;
+  static constexpr int WM = BM / 2, WN = 64;             // 2 x 2 waves
+  static constexpr int TM = WM / 32, TN = 2;             // 32x32 tiles per wave
   static constexpr int kPlane = BM * kLdsRow;
   static constexpr int kABytes = AW * kPlane;
   static constexpr int kStage = kABytes + BN * kLdsRow;
@@ -111,6 +123,8 @@ __device__ __forceinline__ void tile_coords(int v, int nMB, int nNB, int& mb, in
   nb = in / gs;
 }
 
+__device__ __forceinline__ uint32_t pack16(int32_t a, int32_t b) { return (uint32_t)(a & 0xFFFF) | ((uint32_t)b << 16); }
+
 template <int AW, int EPI>
 __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
   using C = GemmCfg<AW>;
@@ -128,7 +142,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
   const int wm = wave >> 1, wn = wave & 1;
   const uint8_t* Ab = (const uint8_t*)g.A;
 
-  // global loads of step s (tile s / nk, k block s % nk) into register set rs
+  // global loads of step s (tile s / nk, k block s % nk) into register set `set`
   uint4 areg[2][C::kAChunks], breg[2][C::kBChunks];
   auto load = [&](int st, int set) {
     const int j = st / nk, kb = st - j * nk;
@@ -143,9 +157,9 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
     }
 #pragma unroll
     for (int i = 0; i < C::kBChunks; ++i) {
-      // weight rows permuted within their 64-row blocks (col_perm)
-      const int wj = (tid + C::kThreads * i) >> 2;
-      const int wrow = n0 + (wj & 64) + col_perm<P>((wj & 63) >> 4, (wj & 15) >> 2, wj & 3);
+      // LDS weight row rho holds global row n0 + 64 (rho / 64) + col_perm(tn, i)
+      const int rho = (tid + C::kThreads * i) >> 2;
+      const int wrow = n0 + (rho & 64) + col_perm<P>((rho >> 5) & 1, rho & 31);
       breg[set][i] = wrow < g.N ? *(const uint4*)(g.W + (size_t)wrow * g.K + (size_t)kb * kBK + (tid & 3) * 16)
                                 : make_uint4(0, 0, 0, 0);
     }
@@ -171,13 +185,13 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
       *(uint4*)(base + C::kABytes + ((tid + C::kThreads * i) >> 2) * kLdsRow + (tid & 3) * 16) = breg[set][i];
   };
 
-  v4i acc[C::TM][C::TN][AW];
+  v16i acc[C::TM][C::TN][AW];
 #pragma unroll
   for (int a = 0; a < C::TM; ++a)
 #pragma unroll
     for (int b = 0; b < C::TN; ++b)
 #pragma unroll
-      for (int l = 0; l < AW; ++l) acc[a][b][l] = v4i{0, 0, 0, 0};
+      for (int l = 0; l < AW; ++l) acc[a][b][l] = v16i{};
 
   // Step s computes from LDS stage s % 2; its global data was loaded two steps earlier into
   // register set s % 2 and stored to LDS during step s - 1.
@@ -185,23 +199,27 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
   if (nsteps > 1) load(1, 1);
   store(0, 0);
   __syncthreads();
-  const int fr = lane & 15, fk = (lane >> 4) * 16;
+  const int fc = lane & 31, fh = lane >> 5;
   // one step; CUR = st % 2 is a compile-time constant so the register sets stay in registers
   auto step = [&](auto CUR, int st) {
     constexpr int cur = decltype(CUR)::value;
     if (st + 2 < nsteps) load(st + 2, cur);
     const uint8_t* base = smem + cur * C::kStage;
-    v4i wf[C::TN];
 #pragma unroll
-    for (int tn = 0; tn < C::TN; ++tn)
-      wf[tn] = *(const v4i*)(base + C::kABytes + (wn * C::WN + tn * 16 + fr) * kLdsRow + fk);
+    for (int ks = 0; ks < 2; ++ks) {
+      const int fk = 32 * ks + 16 * fh;
+      v4i wf[C::TN];
 #pragma unroll
-    for (int tm = 0; tm < C::TM; ++tm) {
+      for (int tn = 0; tn < C::TN; ++tn)
+        wf[tn] = *(const v4i*)(base + C::kABytes + (wn * C::WN + tn * 32 + fc) * kLdsRow + fk);
 #pragma unroll
-      for (int l = 0; l < AW; ++l) {
-        const v4i af = *(const v4i*)(base + l * C::kPlane + (wm * C::WM + tm * 16 + fr) * kLdsRow + fk);
+      for (int tm = 0; tm < C::TM; ++tm) {
 #pragma unroll
-        for (int tn = 0; tn < C::TN; ++tn) acc[tm][tn][l] = mfma(wf[tn], af, acc[tm][tn][l]);
+        for (int l = 0; l < AW; ++l) {
+          const v4i af = *(const v4i*)(base + l * C::kPlane + (wm * C::WM + tm * 32 + fc) * kLdsRow + fk);
+#pragma unroll
+          for (int tn = 0; tn < C::TN; ++tn) acc[tm][tn][l] = mfma32(wf[tn], af, acc[tm][tn][l]);
+        }
       }
     }
     if (st + 1 < nsteps) store(cur ^ 1, cur ^ 1);
@@ -209,162 +227,128 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
     const int j = st / nk;
     if (st - j * nk != nk - 1) return;
 
+    // ---------------------------------------------------------------- epilogue
     int mb, nb;
     tile_coords(v0 + j * nwg_x, nMB, nNB, mb, nb);
     const int m0 = mb * C::BM, n0 = nb * C::BN;
-  // ---------------------------------------------------------------- epilogue
-  const int gq = lane >> 4;
-  const int nblk = n0 + wn * C::WN;                     // first column of this wave's block
-  int mrow[C::TM];
+    const int nblk = n0 + wn * C::WN;                   // first column of this wave's block
+    int mrow[C::TM];
 #pragma unroll
-  for (int tm = 0; tm < C::TM; ++tm) mrow[tm] = m0 + wm * C::WM + tm * 16 + fr;
+    for (int tm = 0; tm < C::TM; ++tm) mrow[tm] = m0 + wm * C::WM + tm * 32 + fc;
+    const int64_t bias = limb_bias(AW);
+    // exact int64 accumulator of register e of tile (tm, tn)
+    auto acc64 = [&](int tm, int tn, int e, int32_t ws) -> int64_t {
+      int64_t a = bias * (int64_t)ws;
+#pragma unroll
+      for (int l = 0; l < AW; ++l) a += (int64_t)acc[tm][tn][l][e] * ((int64_t)1 << (8 * l));
+      return a;
+    };
 
-  if constexpr (EPI == EPI_I64 || EPI == EPI_REQ16 || EPI == EPI_REQ32 || EPI == EPI_RESID || EPI == EPI_LOGITS) {
-    // PERM_CONTIG: lane holds columns nblk + 16 gq + 4 t + r
-    const double lo = EPI == EPI_REQ16 || EPI == EPI_REQ32 ? -ldexp(1.0, g.sat_bits - 1) : 0.0;
-    const double hi = EPI == EPI_REQ16 || EPI == EPI_REQ32 ? ldexp(1.0, g.sat_bits - 1) - 1.0 : 0.0;
+    if constexpr (P == PERM_CONTIG) {
+      // lane holds block columns 32 fh + 16 tn + 4 b + r: groups of 4 consecutive columns
+      const double lo = EPI == EPI_REQ16 || EPI == EPI_REQ32 ? -ldexp(1.0, g.sat_bits - 1) : 0.0;
+      const double hi = EPI == EPI_REQ16 || EPI == EPI_REQ32 ? ldexp(1.0, g.sat_bits - 1) - 1.0 : 0.0;
 #pragma unroll
-    for (int t = 0; t < C::TN; ++t) {
-      const int nc = nblk + 16 * gq + 4 * t;           // 4 consecutive columns nc..nc+3
-      if (nc >= g.N) continue;                          // N is a multiple of 4
-      int4 ws4 = make_int4(0, 0, 0, 0), mu4 = make_int4(0, 0, 0, 0), sh4 = make_int4(1, 1, 1, 1);
-      if constexpr (AW == 4 || EPI == EPI_I64) ws4 = *(const int4*)(g.wsum + nc);
-      if constexpr (AW == 4 && EPI != EPI_I64) { mu4 = *(const int4*)(g.mult + nc); sh4 = *(const int4*)(g.shift + nc); }
-      const int wsv[4] = {ws4.x, ws4.y, ws4.z, ws4.w}, muv[4] = {mu4.x, mu4.y, mu4.z, mu4.w},
-                shv[4] = {sh4.x, sh4.y, sh4.z, sh4.w};
-      if constexpr (AW == 2 && EPI != EPI_I64) {
-        double2 k[4];
+      for (int tn = 0; tn < C::TN; ++tn)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) k[r] = g.coef[nc + r];
+        for (int b = 0; b < 4; ++b) {
+          const int nc = nblk + 32 * fh + 16 * tn + 4 * b;    // columns nc .. nc+3
+          if (nc >= g.N) continue;                              // N is a multiple of 4
+          int4 ws4 = make_int4(0, 0, 0, 0), mu4 = make_int4(0, 0, 0, 0), sh4 = make_int4(1, 1, 1, 1);
+          double2 k[4];
+          if constexpr (AW == 4 || EPI == EPI_I64) ws4 = *(const int4*)(g.wsum + nc);
+          if constexpr (AW == 4 && EPI != EPI_I64) { mu4 = *(const int4*)(g.mult + nc); sh4 = *(const int4*)(g.shift + nc); }
+          if constexpr (AW == 2 && EPI != EPI_I64) {
 #pragma unroll
-        for (int tm = 0; tm < C::TM; ++tm) {
-          const int m = mrow[tm];
-          if (m >= g.M) continue;
-          const size_t o = (size_t)m * g.N + nc;
-          double y[4];
+            for (int r = 0; r < 4; ++r) k[r] = g.coef[nc + r];
+          }
+          const int wsv[4] = {ws4.x, ws4.y, ws4.z, ws4.w}, muv[4] = {mu4.x, mu4.y, mu4.z, mu4.w},
+                    shv[4] = {sh4.x, sh4.y, sh4.z, sh4.w};
 #pragma unroll
-          for (int r = 0; r < 4; ++r) y[r] = req2(acc[tm][t][1][r], acc[tm][t][0][r], k[r]);
-          if constexpr (EPI == EPI_REQ16) {
-            int v[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) v[r] = rne_i32(fmin(fmax(y[r], lo), hi));
-            *(uint2*)((int16_t*)g.out + o) = make_uint2((uint32_t)(v[0] & 0xFFFF) | ((uint32_t)v[1] << 16),
-                                                       (uint32_t)(v[2] & 0xFFFF) | ((uint32_t)v[3] << 16));
-          } else if constexpr (EPI == EPI_REQ32) {
-            int4 v;
-            v.x = rne_i32(fmin(fmax(y[0], lo), hi)); v.y = rne_i32(fmin(fmax(y[1], lo), hi));
-            v.z = rne_i32(fmin(fmax(y[2], lo), hi)); v.w = rne_i32(fmin(fmax(y[3], lo), hi));
-            *(int4*)((int32_t*)g.out + o) = v;
-          } else if constexpr (EPI == EPI_RESID) {
-            int4* xp = (int4*)((int32_t*)g.out + o);
-            const int4 x = *xp;
-            const double xv[4] = {(double)x.x, (double)x.y, (double)x.z, (double)x.w};
-            int v[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-              v[r] = rne_i32(fmin(fmax(rint(y[r]) + xv[r], -2147483648.0), 2147483647.0));
-            *xp = make_int4(v[0], v[1], v[2], v[3]);
-          } else {   // EPI_LOGITS
-            int v[4];
-            bool bad = false;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const double t2 = rint(y[r]);
-              bad |= t2 > 2147483647.0 || t2 < -2147483648.0;
-              v[r] = rne_i32(t2);
+          for (int tm = 0; tm < C::TM; ++tm) {
+            const int m = mrow[tm];
+            if (m >= g.M) continue;
+            const size_t o = (size_t)m * g.N + nc;
+            if constexpr (EPI == EPI_I64) {
+              int64_t* op = (int64_t*)g.out + o;
+              *(longlong2*)op = make_longlong2(acc64(tm, tn, 4 * b, wsv[0]), acc64(tm, tn, 4 * b + 1, wsv[1]));
+              *(longlong2*)(op + 2) = make_longlong2(acc64(tm, tn, 4 * b + 2, wsv[2]), acc64(tm, tn, 4 * b + 3, wsv[3]));
+              continue;
             }
-            if (bad) atomicOr(g.flag, 1);
-            *(int4*)((int32_t*)g.out + o) = make_int4(v[0], v[1], v[2], v[3]);
-          }
-        }
-      } else {
-        const int64_t bias = limb_bias(AW);
-#pragma unroll
-        for (int tm = 0; tm < C::TM; ++tm) {
-          const int m = mrow[tm];
-          if (m >= g.M) continue;
-          const size_t o = (size_t)m * g.N + nc;
-          int64_t a[4];
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            a[r] = bias * (int64_t)wsv[r];
-#pragma unroll
-            for (int l = 0; l < AW; ++l) a[r] += (int64_t)acc[tm][t][l][r] * ((int64_t)1 << (8 * l));
-          }
-          if constexpr (EPI == EPI_I64) {
-            int64_t* op = (int64_t*)g.out + o;
-            *(longlong2*)op = make_longlong2(a[0], a[1]);
-            *(longlong2*)(op + 2) = make_longlong2(a[2], a[3]);
-          } else {
+            // t2[r] = RS(acc * m, sh) as an exact integer-valued double (2 limbs) or int64 (4 limbs)
+            double y[4];
             int64_t v[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) v[r] = rs(a[r] * muv[r], shv[r]);
-            if constexpr (EPI == EPI_REQ16) {
-              *(uint2*)((int16_t*)g.out + o) =
-                  make_uint2((uint32_t)(sat(v[0], g.sat_bits) & 0xFFFF) | ((uint32_t)sat(v[1], g.sat_bits) << 16),
-                             (uint32_t)(sat(v[2], g.sat_bits) & 0xFFFF) | ((uint32_t)sat(v[3], g.sat_bits) << 16));
-            } else if constexpr (EPI == EPI_REQ32) {
-              *(int4*)((int32_t*)g.out + o) = make_int4((int)sat(v[0], g.sat_bits), (int)sat(v[1], g.sat_bits),
-                                                        (int)sat(v[2], g.sat_bits), (int)sat(v[3], g.sat_bits));
+            for (int r = 0; r < 4; ++r) {
+              if constexpr (AW == 2) y[r] = req2(acc[tm][tn][1][4 * b + r], acc[tm][tn][0][4 * b + r], k[r]);
+              else v[r] = rs(acc64(tm, tn, 4 * b + r, wsv[r]) * muv[r], shv[r]);
+            }
+            if constexpr (EPI == EPI_REQ16 || EPI == EPI_REQ32) {
+              int32_t q[4];
+#pragma unroll
+              for (int r = 0; r < 4; ++r)
+                q[r] = AW == 2 ? rne_i32(fmin(fmax(y[r], lo), hi)) : (int32_t)sat(v[r], g.sat_bits);
+              if constexpr (EPI == EPI_REQ16) *(uint2*)((int16_t*)g.out + o) = make_uint2(pack16(q[0], q[1]), pack16(q[2], q[3]));
+              else *(int4*)((int32_t*)g.out + o) = make_int4(q[0], q[1], q[2], q[3]);
             } else if constexpr (EPI == EPI_RESID) {
               int4* xp = (int4*)((int32_t*)g.out + o);
               const int4 x = *xp;
-              *xp = make_int4((int)clamp_bits32((int64_t)x.x + v[0]), (int)clamp_bits32((int64_t)x.y + v[1]),
-                              (int)clamp_bits32((int64_t)x.z + v[2]), (int)clamp_bits32((int64_t)x.w + v[3]));
-            } else {
+              const int32_t xv[4] = {x.x, x.y, x.z, x.w};
+              int32_t q[4];
+#pragma unroll
+              for (int r = 0; r < 4; ++r)
+                q[r] = AW == 2 ? rne_i32(fmin(fmax(rint(y[r]) + (double)xv[r], -2147483648.0), 2147483647.0))
+                               : (int32_t)clamp_bits32((int64_t)xv[r] + v[r]);
+              *xp = make_int4(q[0], q[1], q[2], q[3]);
+            } else {   // EPI_LOGITS
+              int32_t q[4];
               bool bad = false;
 #pragma unroll
-              for (int r = 0; r < 4; ++r) bad |= v[r] != (int64_t)(int32_t)v[r];
+              for (int r = 0; r < 4; ++r) {
+                if constexpr (AW == 2) {
+                  const double t2 = rint(y[r]);
+                  bad |= t2 > 2147483647.0 || t2 < -2147483648.0;
+                  q[r] = rne_i32(t2);
+                } else {
+                  bad |= v[r] != (int64_t)(int32_t)v[r];
+                  q[r] = (int32_t)v[r];
+                }
+              }
               if (bad) atomicOr(g.flag, 1);
-              *(int4*)((int32_t*)g.out + o) = make_int4((int)v[0], (int)v[1], (int)v[2], (int)v[3]);
+              *(int4*)((int32_t*)g.out + o) = make_int4(q[0], q[1], q[2], q[3]);
             }
           }
         }
-      }
-    }
-  } else {
-    // PERM_PAIR: lane holds block-local rows j = 8 gq + 4 (t & 1) + r (t = 0, 1) paired with j + 32
-    // (t = 2, 3): (gate j, up j) for EPI_SILU, (d, d + 32) of one head for EPI_QKV.
-    const int64_t bias = limb_bias(AW);
-    // SAT16(RS(acc * m, sh)) of the lane's value (tm, t, r) in column n
-    auto value16 = [&](int tm, int t, int r, int n) -> int32_t {
-      if constexpr (AW == 2) {
-        return rne_i32(fmin(fmax(req2(acc[tm][t][1][r], acc[tm][t][0][r], g.coef[n]), -32768.0), 32767.0));
-      } else {
-        int64_t a = bias * (int64_t)g.wsum[n];
-#pragma unroll
-        for (int l = 0; l < AW; ++l) a += (int64_t)acc[tm][t][l][r] * ((int64_t)1 << (8 * l));
-        return (int32_t)clamp_bits16(rs(a * g.mult[n], g.shift[n]));
-      }
-    };
-    if (nblk < g.N) {
+    } else if (nblk < g.N) {
+      // PERM_PAIR: lane holds block columns jl = 16 fh + 4 b + r (tn = 0) and jl + 32 (tn = 1):
+      // (gate j, up j) for EPI_SILU, (d, d + 32) of one head for EPI_QKV
+      auto value16 = [&](int tm, int tn, int e, int n) -> int32_t {   // SAT16(RS(acc * m, sh)) of column n
+        if constexpr (AW == 2) {
+          return rne_i32(fmin(fmax(req2(acc[tm][tn][1][e], acc[tm][tn][0][e], g.coef[n]), -32768.0), 32767.0));
+        } else {
+          return (int32_t)clamp_bits16(rs(acc64(tm, tn, e, g.wsum[n]) * g.mult[n], g.shift[n]));
+        }
+      };
       if constexpr (EPI == EPI_SILU) {
-        // gated[m, j]: j = 32 * (nblk / 64) + 8 gq + 4 t + r, t = 0, 1; weight rows nblk + j' and nblk + 32 + j'
-        const int jb = (nblk >> 6) * 32 + 8 * gq;
         const double lo = -ldexp(1.0, g.bits2 - 1), hi = ldexp(1.0, g.bits2 - 1) - 1.0;
+        const int jg = (nblk >> 6) * 32 + 16 * fh;          // gated column of jl = 16 fh
 #pragma unroll
         for (int tm = 0; tm < C::TM; ++tm) {
           const int m = mrow[tm];
           if (m >= g.M) continue;
-          int32_t v[8];
 #pragma unroll
-          for (int t = 0; t < 2; ++t)
+          for (int b = 0; b < 4; ++b) {
+            int32_t v[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-              const int jl = 8 * gq + 4 * t + r;
-              const int32_t gv = value16(tm, t, r, nblk + jl);
-              const int32_t uv = value16(tm, t + 2, r, nblk + 32 + jl);
-              const double sg = (double)g.aux_tab[gv + 32768];
-              v[4 * t + r] = rs_sat_f64(sg * (double)uv, g.sh2, lo, hi);
+              const int jl = 16 * fh + 4 * b + r;
+              const int32_t gv = value16(tm, 0, 4 * b + r, nblk + jl);
+              const int32_t uv = value16(tm, 1, 4 * b + r, nblk + 32 + jl);
+              v[r] = rs_sat_f64((double)g.aux_tab[gv + 32768] * (double)uv, g.sh2, lo, hi);
             }
-          const size_t o = (size_t)m * (g.N / 2) + jb;
-          if (g.bits2 == 16) {
-            *(uint4*)((int16_t*)g.out + o) = make_uint4(
-                (uint32_t)(v[0] & 0xFFFF) | ((uint32_t)v[1] << 16), (uint32_t)(v[2] & 0xFFFF) | ((uint32_t)v[3] << 16),
-                (uint32_t)(v[4] & 0xFFFF) | ((uint32_t)v[5] << 16), (uint32_t)(v[6] & 0xFFFF) | ((uint32_t)v[7] << 16));
-          } else {
-            *(int4*)((int32_t*)g.out + o) = make_int4(v[0], v[1], v[2], v[3]);
-            *(int4*)((int32_t*)g.out + o + 4) = make_int4(v[4], v[5], v[6], v[7]);
+            const size_t o = (size_t)m * (g.N / 2) + jg + 4 * b;
+            if (g.bits2 == 16) *(uint2*)((int16_t*)g.out + o) = make_uint2(pack16(v[0], v[1]), pack16(v[2], v[3]));
+            else *(int4*)((int32_t*)g.out + o) = make_int4(v[0], v[1], v[2], v[3]);
           }
         }
       } else {   // EPI_QKV: heads 0..8 q and 9..11 k get RoPE, 12..14 v are stored as they are
@@ -374,41 +358,37 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
         for (int tm = 0; tm < C::TM; ++tm) {
           const int m = mrow[tm];
           if (m >= g.M) continue;
-          int32_t lo8[8], hi8[8];
           const int ps = head < 12 ? g.pos[m] : 0;
+          int16_t* op = (int16_t*)g.out + (size_t)m * g.N + nblk + 16 * fh;
 #pragma unroll
-          for (int t = 0; t < 2; ++t)
+          for (int b = 0; b < 4; ++b) {
+            int32_t lo4[4], hi4[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-              const int d = 8 * gq + 4 * t + r;
-              const int32_t a1 = value16(tm, t, r, nblk + d), a2 = value16(tm, t + 2, r, nblk + 32 + d);
+              const int d = 16 * fh + 4 * b + r;
+              const int32_t a1 = value16(tm, 0, 4 * b + r, nblk + d), a2 = value16(tm, 1, 4 * b + r, nblk + 32 + d);
               if (head < 12) {
                 const double c = (double)g.cosT[ps * 32 + d], sn = (double)g.sinT[ps * 32 + d];
                 const double o1 = fma((double)a1, c, -(double)a2 * sn), o2 = fma((double)a2, c, (double)a1 * sn);
-                lo8[4 * t + r] = rs_sat_f64(o1, shr, -32768.0, 32767.0);
-                hi8[4 * t + r] = rs_sat_f64(o2, shr, -32768.0, 32767.0);
+                lo4[r] = rs_sat_f64(o1, shr, -32768.0, 32767.0);
+                hi4[r] = rs_sat_f64(o2, shr, -32768.0, 32767.0);
               } else {
-                lo8[4 * t + r] = a1;
-                hi8[4 * t + r] = a2;
+                lo4[r] = a1;
+                hi4[r] = a2;
               }
             }
-          int16_t* op = (int16_t*)g.out + (size_t)m * g.N + nblk + 8 * gq;
-          *(uint4*)op = make_uint4(
-              (uint32_t)(lo8[0] & 0xFFFF) | ((uint32_t)lo8[1] << 16), (uint32_t)(lo8[2] & 0xFFFF) | ((uint32_t)lo8[3] << 16),
-              (uint32_t)(lo8[4] & 0xFFFF) | ((uint32_t)lo8[5] << 16), (uint32_t)(lo8[6] & 0xFFFF) | ((uint32_t)lo8[7] << 16));
-          *(uint4*)(op + 32) = make_uint4(
-              (uint32_t)(hi8[0] & 0xFFFF) | ((uint32_t)hi8[1] << 16), (uint32_t)(hi8[2] & 0xFFFF) | ((uint32_t)hi8[3] << 16),
-              (uint32_t)(hi8[4] & 0xFFFF) | ((uint32_t)hi8[5] << 16), (uint32_t)(hi8[6] & 0xFFFF) | ((uint32_t)hi8[7] << 16));
+            *(uint2*)(op + 4 * b) = make_uint2(pack16(lo4[0], lo4[1]), pack16(lo4[2], lo4[3]));
+            *(uint2*)(op + 32 + 4 * b) = make_uint2(pack16(hi4[0], hi4[1]), pack16(hi4[2], hi4[3]));
+          }
         }
       }
     }
-  }
 #pragma unroll
     for (int a = 0; a < C::TM; ++a)
 #pragma unroll
       for (int b = 0; b < C::TN; ++b)
 #pragma unroll
-        for (int l = 0; l < AW; ++l) acc[a][b][l] = v4i{0, 0, 0, 0};
+        for (int l = 0; l < AW; ++l) acc[a][b][l] = v16i{};
   };
   for (int st = 0; st < nsteps; st += 2) {
     step(std::integral_constant<int, 0>{}, st);

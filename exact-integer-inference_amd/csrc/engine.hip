@@ -497,18 +497,10 @@ int set_batch(eii_model* m, const std::vector<int32_t>& lens, hipStream_t s) {
   return EII_OK;
 }
 
-int gemm_req(const Mat& W, const void* A, int a_bytes, int M, void* out, int out_bits, hipStream_t s) {
-  GemmArgs g{A, W.W, M, W.N, W.K, W.wsum, W.mult, W.shift, out, out_bits, nullptr};
+GemmArgs gemm_args(const Mat& W, const void* planes, int M, void* out, int sat_bits) {
+  GemmArgs g{planes, W.W, M, W.N, W.K, (size_t)M * W.K, W.wsum, W.mult, W.shift, out, sat_bits, nullptr};
   g.coef = W.coef;
-  HIPCHK(gemm(g, a_bytes, out_bits == 16 ? EPI_REQ16 : EPI_REQ32, s));
-  return EII_OK;
-}
-
-int gemm_resid(const Mat& W, const void* A, int a_bytes, int M, int32_t* x, hipStream_t s) {
-  GemmArgs g{A, W.W, M, W.N, W.K, W.wsum, W.mult, W.shift, x, 32, nullptr};
-  g.coef = W.coef;
-  HIPCHK(gemm(g, a_bytes, EPI_RESID, s));
-  return EII_OK;
+  return g;
 }
 
 hipError_t copy_cols(void* dst, int dst_w, const void* src, int src_w, int col0, int ncols, int esz, int rows,
@@ -517,24 +509,30 @@ hipError_t copy_cols(void* dst, int dst_w, const void* src, int src_w, int col0,
                           (size_t)ncols * esz, rows, hipMemcpyDeviceToDevice, s);
 }
 
+// One decoder block (python/intref.py:192-286) on x [M, 576].  Norm outputs, the attention
+// context and the gated product live in m->h, m->ctx and m->gated as int8 limb planes; with a
+// trace the unfused q/k/v and gate/up projections run so their values can be dumped, and the
+// producers also write plain copies into the trace buffers.
 int run_block(eii_model* m, int l, int32_t* x, int M, int nseq, int max_T, const eii_trace* tr, hipStream_t s) {
   const Layer& L = m->L[l];
   const int hb = L.bits[NORM1] / 8;
-  int rc;
+  uint8_t* h = (uint8_t*)m->h;
   {
     ProfScope ps(m, EII_K_NORM, s);
-    HIPCHK(rmsnorm(x, M, L.ln1, 21 + L.ln1_f - L.f[NORM1], L.bits[NORM1], m->h, hb, s));
+    HIPCHK(rmsnorm(x, M, L.ln1, 21 + L.ln1_f - L.f[NORM1], L.bits[NORM1], h, tr ? tr->norm1_out : nullptr, s));
   }
-  if (tr && tr->norm1_out) HIPCHK(hipMemcpyAsync(tr->norm1_out, m->h, (size_t)M * kD * hb, hipMemcpyDeviceToDevice, s));
   const int sh_q = 30 + L.f[QP] - L.f[QR], sh_k = 30 + L.f[KP] - L.f[KR];
-  if (!tr) {
-    // q, k, v projections with RoPE applied in the epilogue
+  {
     ProfScope ps(m, EII_K_GEMM_QKV, s);
-    GemmArgs g{m->h, L.qkv.W, M, L.qkv.N, L.qkv.K, L.qkv.wsum, L.qkv.mult, L.qkv.shift, m->qkv, 16, nullptr};
-    g.pos = m->pos; g.cosT = m->rope_c; g.sinT = m->rope_s; g.sh_q = sh_q; g.sh_k = sh_k; g.coef = L.qkv.coef;
-    HIPCHK(gemm(g, hb, EPI_QKV, s));
-  } else {
-    if ((rc = gemm_req(L.qkv, m->h, hb, M, m->qkv, 16, s))) return rc;
+    GemmArgs g = gemm_args(L.qkv, h, M, m->qkv, 16);
+    if (!tr) {   // q, k, v projections with RoPE applied in the epilogue
+      g.pos = m->pos; g.cosT = m->rope_c; g.sinT = m->rope_s; g.sh_q = sh_q; g.sh_k = sh_k;
+      HIPCHK(gemm(g, hb, EPI_QKV, s));
+    } else {
+      HIPCHK(gemm(g, hb, EPI_REQ16, s));
+    }
+  }
+  if (tr) {
     if (tr->q_proj) HIPCHK(copy_cols(tr->q_proj, kD, m->qkv, kQKVN, 0, kD, 2, M, s));
     if (tr->k_proj) HIPCHK(copy_cols(tr->k_proj, 192, m->qkv, kQKVN, kD, 192, 2, M, s));
     if (tr->v_proj) HIPCHK(copy_cols(tr->v_proj, 192, m->qkv, kQKVN, kD + 192, 192, 2, M, s));
@@ -542,47 +540,47 @@ int run_block(eii_model* m, int l, int32_t* x, int M, int nseq, int max_T, const
     if (tr->q_rope) HIPCHK(copy_cols(tr->q_rope, kD, m->qkv, kQKVN, 0, kD, 2, M, s));
     if (tr->k_rope) HIPCHK(copy_cols(tr->k_rope, 192, m->qkv, kQKVN, kD, 192, 2, M, s));
   }
-  AttnArgs a{m->qkv, m->seq_off, m->exp_tab, m->ctx, nseq, max_T, L.f[QR] + L.f[KR] + 3 - kFScore,
-             16 + L.f[VP] - L.f[CTX], L.bits[CTX]};
   const int cb = L.bits[CTX] / 8;
   {
     ProfScope ps(m, EII_K_ATTN, s);
-    HIPCHK(attention(a, cb, s));
+    AttnArgs a{m->qkv, m->seq_off, m->exp_tab, tr ? tr->attn_ctx : nullptr, (uint8_t*)m->ctx, M, nseq, max_T,
+               L.f[QR] + L.f[KR] + 3 - kFScore, 16 + L.f[VP] - L.f[CTX], L.bits[CTX]};
+    HIPCHK(attention(a, s));
   }
-  if (tr && tr->attn_ctx) HIPCHK(hipMemcpyAsync(tr->attn_ctx, m->ctx, (size_t)M * kD * cb, hipMemcpyDeviceToDevice, s));
   {
     ProfScope ps(m, EII_K_GEMM_O, s);
-    if ((rc = gemm_resid(L.o, m->ctx, cb, M, x, s))) return rc;
+    HIPCHK(gemm(gemm_args(L.o, m->ctx, M, x, 32), cb, EPI_RESID, s));
   }
   if (tr && tr->resid_mid) HIPCHK(hipMemcpyAsync(tr->resid_mid, x, (size_t)M * kD * 4, hipMemcpyDeviceToDevice, s));
   const int h2b = L.bits[NORM2] / 8;
   {
     ProfScope ps(m, EII_K_NORM, s);
-    HIPCHK(rmsnorm(x, M, L.ln2, 21 + L.ln2_f - L.f[NORM2], L.bits[NORM2], m->h, h2b, s));
+    HIPCHK(rmsnorm(x, M, L.ln2, 21 + L.ln2_f - L.f[NORM2], L.bits[NORM2], h, tr ? tr->norm2_out : nullptr, s));
   }
-  if (tr && tr->norm2_out) HIPCHK(hipMemcpyAsync(tr->norm2_out, m->h, (size_t)M * kD * h2b, hipMemcpyDeviceToDevice, s));
   const int gb = L.bits[GATED] / 8;
   const int sh_s = L.f[SILU] + L.f[UP] - L.f_m;
-  if (!tr) {
-    // gate and up projections with the SiLU table and the gated product in the epilogue
+  {
     ProfScope ps(m, EII_K_GEMM_GU, s);
-    GemmArgs g{m->h, L.gu.W, M, L.gu.N, L.gu.K, L.gu.wsum, L.gu.mult, L.gu.shift, m->gated, 16, nullptr};
-    g.aux_tab = L.silu; g.sh2 = sh_s; g.bits2 = L.bits[GATED]; g.coef = L.gu.coef;
-    HIPCHK(gemm(g, h2b, EPI_SILU, s));
-  } else {
-    if ((rc = gemm_req(L.gu, m->h, h2b, M, m->gu, 16, s))) return rc;
+    if (!tr) {   // gate and up projections with the SiLU table and the gated product in the epilogue
+      GemmArgs g = gemm_args(L.gu, h, M, m->gated, 16);
+      g.aux_tab = L.silu; g.sh2 = sh_s; g.bits2 = L.bits[GATED];
+      HIPCHK(gemm(g, h2b, EPI_SILU, s));
+    } else {
+      HIPCHK(gemm(gemm_args(L.gu, h, M, m->gu, 16), h2b, EPI_REQ16, s));
+    }
+  }
+  if (tr) {
     // gu holds [gate 32 | up 32] blocks; de-interleave for the dumps
     if (tr->gate_proj)
       HIPCHK(hipMemcpy2DAsync(tr->gate_proj, 64, m->gu, 128, 64, (size_t)M * 48, hipMemcpyDeviceToDevice, s));
     if (tr->up_proj)
       HIPCHK(hipMemcpy2DAsync(tr->up_proj, 64, (const uint8_t*)m->gu + 64, 128, 64, (size_t)M * 48,
                               hipMemcpyDeviceToDevice, s));
-    HIPCHK(silu_gate(m->gu, M, L.silu, sh_s, L.bits[GATED], m->gated, gb, s));
+    HIPCHK(silu_gate(m->gu, M, L.silu, sh_s, L.bits[GATED], (uint8_t*)m->gated, tr->mlp_gated, s));
   }
-  if (tr && tr->mlp_gated) HIPCHK(hipMemcpyAsync(tr->mlp_gated, m->gated, (size_t)M * kDFF * gb, hipMemcpyDeviceToDevice, s));
   {
     ProfScope ps(m, EII_K_GEMM_DOWN, s);
-    if ((rc = gemm_resid(L.down, m->gated, gb, M, x, s))) return rc;
+    HIPCHK(gemm(gemm_args(L.down, m->gated, M, x, 32), gb, EPI_RESID, s));
   }
   return EII_OK;
 }
@@ -590,10 +588,10 @@ int run_block(eii_model* m, int l, int32_t* x, int M, int nseq, int max_T, const
 int run_final(eii_model* m, const int32_t* x, int M, int32_t* logits, hipStream_t s) {
   {
     ProfScope ps(m, EII_K_NORM, s);
-    HIPCHK(rmsnorm(x, M, m->fg, 21 + m->fg_f - m->f_y, 16, m->h, 2, s));
+    HIPCHK(rmsnorm(x, M, m->fg, 21 + m->fg_f - m->f_y, 16, (uint8_t*)m->h, nullptr, s));
   }
-  GemmArgs g{m->h, m->head.W, M, kV, kD, m->head.wsum, m->head.mult, m->head.shift, logits, 32, m->flags};
-  g.coef = m->head.coef;
+  GemmArgs g = gemm_args(m->head, m->h, M, logits, 32);
+  g.flag = m->flags;
   ProfScope ps(m, EII_K_GEMM_HEAD, s);
   HIPCHK(gemm(g, 2, EPI_LOGITS, s));
   return EII_OK;
@@ -732,13 +730,31 @@ static int check_gemm_args(const void* A, int a_bits, const int8_t* W, int M, in
   return EII_OK;
 }
 
+// Splits plain A [M, K] into a stream-ordered temporary of limb planes (freed on the stream).
+static int split_temp(const void* A, int a_bits, int M, int K, uint8_t** planes, hipStream_t s) {
+  const size_t n = (size_t)M * K;
+  HIPCHK(hipMallocAsync((void**)planes, n * (a_bits / 8), s));
+  hipError_t e = split_limbs(A, a_bits / 8, n, *planes, s);
+  if (e != hipSuccess) {
+    (void)hipFreeAsync(*planes, s);
+    return fail(EII_E_DEVICE, std::string("limb split: ") + hipGetErrorString(e));
+  }
+  return EII_OK;
+}
+
 extern "C" int eii_gemm_i8_ws(const void* A, int a_bits, const int8_t* W, const int32_t* wsum, int M, int N, int K,
                               int64_t* acc, void* stream) {
   int rc;
   if ((rc = check_gemm_args(A, a_bits, W, M, N, K))) return rc;
   if (!wsum || !acc) return fail(EII_E_ARG, "null output");
-  GemmArgs g{A, W, M, N, K, wsum, nullptr, nullptr, acc, 64, nullptr};
-  HIPCHK(gemm(g, a_bits / 8, EPI_I64, (hipStream_t)stream));
+  if (N % 4) return fail(EII_E_ARG, "N must be a multiple of 4");
+  hipStream_t s = (hipStream_t)stream;
+  uint8_t* planes = nullptr;
+  if ((rc = split_temp(A, a_bits, M, K, &planes, s))) return rc;
+  GemmArgs g{planes, W, M, N, K, (size_t)M * K, wsum, nullptr, nullptr, acc, 64, nullptr};
+  hipError_t e = gemm(g, a_bits / 8, EPI_I64, s);
+  (void)hipFreeAsync(planes, s);
+  if (e != hipSuccess) return fail(EII_E_DEVICE, std::string("eii_gemm_i8: ") + hipGetErrorString(e));
   return EII_OK;
 }
 
@@ -763,17 +779,21 @@ extern "C" int eii_linear(const void* A, int a_bits, const int8_t* W, const int3
   if ((rc = check_gemm_args(A, a_bits, W, M, N, K))) return rc;
   if (!wsum || !mult || !shift || !out) return fail(EII_E_ARG, "null argument");
   if (out_bits != 16 && out_bits != 32) return fail(EII_E_ARG, "out_bits must be 16 or 32");
+  if (N % 4) return fail(EII_E_ARG, "N must be a multiple of 4");
   hipStream_t s = (hipStream_t)stream;
-  GemmArgs g{A, W, M, N, K, wsum, mult, shift, out, out_bits, nullptr};
+  uint8_t* planes = nullptr;
+  if ((rc = split_temp(A, a_bits, M, K, &planes, s))) return rc;
+  GemmArgs g{planes, W, M, N, K, (size_t)M * K, wsum, mult, shift, out, out_bits, nullptr};
   double2* coef = nullptr;
+  hipError_t e = hipSuccess;
   if (a_bits == 16) {
-    HIPCHK(hipMallocAsync((void**)&coef, (size_t)N * sizeof(double2), s));
-    hipError_t e = gemm_coef(mult, shift, wsum, N, coef, s);
-    if (e != hipSuccess) { (void)hipFreeAsync(coef, s); return fail(EII_E_DEVICE, hipGetErrorString(e)); }
+    e = hipMallocAsync((void**)&coef, (size_t)N * sizeof(double2), s);
+    if (e == hipSuccess) e = gemm_coef(mult, shift, wsum, N, coef, s);
     g.coef = coef;
   }
-  hipError_t e = gemm(g, a_bits / 8, out_bits == 16 ? EPI_REQ16 : EPI_REQ32, s);
+  if (e == hipSuccess) e = gemm(g, a_bits / 8, out_bits == 16 ? EPI_REQ16 : EPI_REQ32, s);
   if (coef) (void)hipFreeAsync(coef, s);
+  (void)hipFreeAsync(planes, s);
   if (e != hipSuccess) return fail(EII_E_DEVICE, std::string("eii_linear: ") + hipGetErrorString(e));
   return EII_OK;
 }
@@ -784,7 +804,7 @@ extern "C" int eii_rmsnorm(const int32_t* x, int M, const int32_t* gain, int f_g
   if (out_bits != 16 && out_bits != 32) return fail(EII_E_ARG, "out_bits must be 16 or 32");
   int rc;
   if ((rc = check_scalar_shift(21 + f_gain - f_out, "norm"))) return rc;
-  HIPCHK(rmsnorm(x, M, gain, 21 + f_gain - f_out, out_bits, out, out_bits / 8, (hipStream_t)stream));
+  HIPCHK(rmsnorm(x, M, gain, 21 + f_gain - f_out, out_bits, nullptr, out, (hipStream_t)stream));
   return EII_OK;
 }
 
@@ -795,7 +815,7 @@ extern "C" int eii_attention(const int16_t* qkv, const int32_t* seq_off, int nse
   const int shift_s = f_qr + f_kr + 3 - kFScore;
   if (shift_s < 1) return fail(EII_E_BOUND, "score shift < 1");
   if (max_T > 16384) return fail(EII_E_BOUND, "sequences longer than 16384 tokens are not supported");
-  AttnArgs a{qkv, seq_off, exp_tab, ctx, nseq, max_T, shift_s, 16 + f_v - f_c, bits_c};
-  HIPCHK(attention(a, bits_c / 8, (hipStream_t)stream));
+  AttnArgs a{qkv, seq_off, exp_tab, ctx, nullptr, 0, nseq, max_T, shift_s, 16 + f_v - f_c, bits_c};
+  HIPCHK(attention(a, (hipStream_t)stream));
   return EII_OK;
 }

@@ -12,7 +12,7 @@ enum Epi : int {
   EPI_REQ32 = 2,   // out int32 [M, N] = SAT(RS(acc * m[n], sh[n]), sat_bits)
   EPI_RESID = 3,   // x int32 [M, N] = SAT32(x + RS(acc * m[n], sh[n]))
   EPI_LOGITS = 4,  // out int32 [M, N] = RS(acc * m[n], sh[n]); *flag |= 1 if it leaves int32
-  // W = blocks of [32 gate rows | 32 up rows] (N = 2 * 1536): out [M, N/2] of bits2 =
+  // W = blocks of [32 gate rows | 32 up rows] (N = 2 * 1536): out = limb planes [bits2/8][M][N/2] of
   //   SAT(RS(aux_tab[SAT16(gate) + 32768] * SAT16(up), sh2), bits2)        (python/intref.py:268-275)
   EPI_SILU = 5,
   // W = q | k | v rows (N = 960, 16-bit outputs): RoPE on q heads (shift sh_q) and k heads (sh_k)
@@ -20,10 +20,13 @@ enum Epi : int {
   EPI_QKV = 6,
 };
 
+// Activations enter the GEMM as int8 limb planes (eii_int.h split_limbs): a_bytes planes of
+// [M, K] bytes, plane l at A + l * a_plane, lowest byte first.
 struct GemmArgs {
-  const void* A;          // activations [M, K], int16 (a_bytes 2) or int32 (a_bytes 4)
+  const void* A;          // limb planes of the [M, K] activations, 2 (16-bit) or 4 (32-bit) planes
   const int8_t* W;        // weights [N, K], row = output channel
   int M, N, K;            // K % 64 == 0
+  size_t a_plane;         // bytes between limb planes (M * K for a dense [L][M][K] layout)
   const int32_t* wsum;    // [N] sum_k W[n, k]
   const int32_t* mult;    // [N] m (|m| <= 2^14)
   const int32_t* shift;   // [N] requantization shift, 1..62
@@ -52,9 +55,13 @@ hipError_t gemm_coef(const int32_t* mult, const int32_t* shift, const int32_t* w
 hipError_t embed(const int64_t* ids, int M, const int8_t* emb_q, const int32_t* emb_m,
                  const int32_t* emb_sh, int32_t* x, int* flag, hipStream_t s);
 
-// out = SAT(RS(3 * RS(x * U, 16) * gain, sh_out), bits_out), out int16 or int32 by out_bytes
+// out = SAT(RS(3 * RS(x * U, 16) * gain, sh_out), bits_out) as limb planes [bits/8][M][576]
+// and/or plain int16/int32 [M, 576] (either pointer may be null)
 hipError_t rmsnorm(const int32_t* x, int M, const int32_t* gain, int sh_out, int bits_out,
-                   void* out, int out_bytes, hipStream_t s);
+                   uint8_t* planes, void* plain, hipStream_t s);
+
+// n values int16 (a_bytes 2) or int32 (a_bytes 4) -> limb planes [a_bytes][n]
+hipError_t split_limbs(const void* a, int a_bytes, size_t n, uint8_t* planes, hipStream_t s);
 
 // In-place rotate-half RoPE on the q (cols 0..575) and k (cols 576..767) parts of qkv [M, 960]
 hipError_t rope(int16_t* qkv, int M, const int32_t* pos, const int32_t* cosT, const int32_t* sinT,
@@ -63,18 +70,20 @@ hipError_t rope(int16_t* qkv, int M, const int32_t* pos, const int32_t* cosT, co
 // gated[m, j] = SAT(RS(silu[gate + 32768] * up, sh), bits) with gu rows holding [gate 32 | up 32]
 // blocks: gate j at column 64 (j / 32) + j % 32, up j 32 columns further
 hipError_t silu_gate(const int16_t* gu, int M, const int32_t* silu, int sh, int bits,
-                     void* gated, int out_bytes, hipStream_t s);
+                     uint8_t* planes, void* plain, hipStream_t s);
 
 struct AttnArgs {
   const int16_t* qkv;      // [M, 960]: q rope | k rope | v
   const int32_t* seq_off;  // [B + 1] row offsets of the sequences
   const int32_t* exp_tab;  // [1537]
-  void* ctx;               // [M, 576], int16 or int32
+  void* ctx;               // plain [M, 576], int16 or int32, or null
+  uint8_t* ctx_planes;     // limb planes [bits_c/8][M][576], or null
+  int M;
   int B, max_T;
   int shift_s;             // f_qr + f_kr + 3 - 7
   int sh_ctx;              // 16 + f_v - f_c
   int bits_c;
 };
-hipError_t attention(const AttnArgs& a, int out_bytes, hipStream_t s);
+hipError_t attention(const AttnArgs& a, hipStream_t s);
 
 }  // namespace eii

@@ -14,6 +14,7 @@
 #include "kernels.h"
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));   // 16-byte staging registers
 
 namespace eii {
 
@@ -39,6 +40,18 @@ __device__ __forceinline__ uint32_t byte_plane32(uint4 d, int i) {
   uint32_t r = ((d.x >> s) & 0xFFu) | (((d.y >> s) & 0xFFu) << 8) | (((d.z >> s) & 0xFFu) << 16) |
                (((d.w >> s) & 0xFFu) << 24);
   return i == 3 ? r : (r ^ 0x80808080u);
+}
+
+// Limb byte l of a W-byte activation v (eii_int.h split_limbs): low bytes biased by -128, the top
+// byte signed.
+__device__ __forceinline__ uint32_t limb_byte(int32_t v, int l, int W) {
+  const uint32_t b = ((uint32_t)v >> (8 * l)) & 0xFFu;
+  return l == W - 1 ? b : (b ^ 0x80u);
+}
+// The 4 limb-l bytes of 4 consecutive values, packed little-endian.
+__device__ __forceinline__ uint32_t limb_word(const int32_t* v, int l, int W) {
+  return limb_byte(v[0], l, W) | (limb_byte(v[1], l, W) << 8) | (limb_byte(v[2], l, W) << 16) |
+         (limb_byte(v[3], l, W) << 24);
 }
 
 // ------------------------------------------------------------------------------ GEMM
@@ -105,7 +118,7 @@ struct GemmCfg {
   static constexpr int kPlane = BM * kLdsRow;
   static constexpr int kABytes = AW * kPlane;
   static constexpr int kStage = kABytes + BN * kLdsRow;
-  static constexpr int kAChunks = BM * 4 * AW / kThreads;   // 16-byte global loads per thread
+  static constexpr int kAChunks = AW * BM * 4 / kThreads;   // 16-byte global loads per thread
   static constexpr int kBChunks = BN * 4 / kThreads;
   static_assert(kAChunks * kThreads == BM * 4 * AW && kBChunks * kThreads == BN * 4, "chunk split");
 };
@@ -142,47 +155,55 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
   const int wm = wave >> 1, wn = wave & 1;
   const uint8_t* Ab = (const uint8_t*)g.A;
 
-  // global loads of step s (tile s / nk, k block s % nk) into register set `set`
-  uint4 areg[2][C::kAChunks], breg[2][C::kBChunks];
-  auto load = [&](int st, int set) {
-    const int j = st / nk, kb = st - j * nk;
+  // Load cursor: the tile and K block of the next step to load, with this thread's source
+  // pointers for that tile (advanced incrementally; divisions happen once per tile).
+  int l_tile = 0, l_kb = 0;
+  const uint8_t* a_src[C::kAChunks];
+  const int8_t* w_src[C::kBChunks];
+  auto set_load_tile = [&](int j) {
     int mb, nb;
     tile_coords(v0 + j * nwg_x, nMB, nNB, mb, nb);
     const int m0 = mb * C::BM, n0 = nb * C::BN;
 #pragma unroll
     for (int i = 0; i < C::kAChunks; ++i) {
-      const int q = tid + C::kThreads * i, row = q / (4 * AW), c = q % (4 * AW), m = m0 + row;
-      areg[set][i] = m < g.M ? *(const uint4*)(Ab + ((size_t)m * g.K + (size_t)kb * kBK) * AW + c * 16)
-                             : make_uint4(0, 0, 0, 0);
+      // chunk q: limb plane l, row, 16-byte chunk c; rows past M read row M - 1 (never stored)
+      const int q = tid + C::kThreads * i, l = q / (4 * C::BM), row = (q >> 2) % C::BM, c = q & 3;
+      const int m = min(m0 + row, g.M - 1);
+      a_src[i] = Ab + (size_t)l * g.a_plane + (size_t)m * g.K + c * 16;
     }
 #pragma unroll
     for (int i = 0; i < C::kBChunks; ++i) {
-      // LDS weight row rho holds global row n0 + 64 (rho / 64) + col_perm(tn, i)
+      // LDS weight row rho holds global row n0 + 64 (rho / 64) + col_perm(tn, i); rows past N read
+      // row N - 1 (their columns are never stored)
       const int rho = (tid + C::kThreads * i) >> 2;
-      const int wrow = n0 + (rho & 64) + col_perm<P>((rho >> 5) & 1, rho & 31);
-      breg[set][i] = wrow < g.N ? *(const uint4*)(g.W + (size_t)wrow * g.K + (size_t)kb * kBK + (tid & 3) * 16)
-                                : make_uint4(0, 0, 0, 0);
+      const int wrow = min(n0 + (rho & 64) + col_perm<P>((rho >> 5) & 1, rho & 31), g.N - 1);
+      w_src[i] = g.W + (size_t)wrow * g.K + (tid & 3) * 16;
     }
   };
-  auto store = [&](int stage, int set) {
-    uint8_t* base = smem + stage * C::kStage;
+  u32x4 areg[2][C::kAChunks], breg[2][C::kBChunks];
+  auto load = [&](auto SET) {   // the step at the cursor, into register set SET (compile time)
+    constexpr int set = decltype(SET)::value;
+    const int kw = l_kb * kBK;
+#pragma unroll
+    for (int i = 0; i < C::kAChunks; ++i) areg[set][i] = *(const u32x4*)(a_src[i] + kw);
+#pragma unroll
+    for (int i = 0; i < C::kBChunks; ++i) breg[set][i] = *(const u32x4*)(w_src[i] + kw);
+    if (++l_kb == nk) {
+      l_kb = 0;
+      if (++l_tile < ntiles) set_load_tile(l_tile);
+    }
+  };
+  auto store = [&](auto SET) {   // register set SET into LDS stage SET
+    constexpr int set = decltype(SET)::value;
+    uint8_t* base = smem + set * C::kStage;
 #pragma unroll
     for (int i = 0; i < C::kAChunks; ++i) {
-      const int q = tid + C::kThreads * i, row = q / (4 * AW), c = q % (4 * AW);
-      const uint4 d = areg[set][i];
-      if constexpr (AW == 2) {
-        uint8_t* p = base + row * kLdsRow + c * 8;
-        *(uint2*)(p) = make_uint2(lo_bytes16(d.x, d.y), lo_bytes16(d.z, d.w));
-        *(uint2*)(p + C::kPlane) = make_uint2(hi_bytes16(d.x, d.y), hi_bytes16(d.z, d.w));
-      } else {
-        uint8_t* p = base + row * kLdsRow + c * 4;
-#pragma unroll
-        for (int pl = 0; pl < 4; ++pl) *(uint32_t*)(p + pl * C::kPlane) = byte_plane32(d, pl);
-      }
+      const int q = tid + C::kThreads * i, l = q / (4 * C::BM), row = (q >> 2) % C::BM, c = q & 3;
+      *(u32x4*)(base + l * C::kPlane + row * kLdsRow + c * 16) = areg[set][i];
     }
 #pragma unroll
     for (int i = 0; i < C::kBChunks; ++i)
-      *(uint4*)(base + C::kABytes + ((tid + C::kThreads * i) >> 2) * kLdsRow + (tid & 3) * 16) = breg[set][i];
+      *(u32x4*)(base + C::kABytes + ((tid + C::kThreads * i) >> 2) * kLdsRow + (tid & 3) * 16) = breg[set][i];
   };
 
   v16i acc[C::TM][C::TN][AW];
@@ -195,15 +216,20 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
 
   // Step s computes from LDS stage s % 2; its global data was loaded two steps earlier into
   // register set s % 2 and stored to LDS during step s - 1.
-  load(0, 0);
-  if (nsteps > 1) load(1, 1);
-  store(0, 0);
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  set_load_tile(0);
+  load(I0{});
+  if (nsteps > 1) load(I1{});
+  store(I0{});
   __syncthreads();
   const int fc = lane & 31, fh = lane >> 5;
+  int c_tile = 0, c_kb = 0;   // tile and K block being computed
   // one step; CUR = st % 2 is a compile-time constant so the register sets stay in registers
   auto step = [&](auto CUR, int st) {
     constexpr int cur = decltype(CUR)::value;
-    if (st + 2 < nsteps) load(st + 2, cur);
+    using NXT = std::integral_constant<int, cur ^ 1>;
+    if (st + 2 < nsteps) load(CUR);
     const uint8_t* base = smem + cur * C::kStage;
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
@@ -222,10 +248,11 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
         }
       }
     }
-    if (st + 1 < nsteps) store(cur ^ 1, cur ^ 1);
+    if (st + 1 < nsteps) store(NXT{});
     __syncthreads();
-    const int j = st / nk;
-    if (st - j * nk != nk - 1) return;
+    if (++c_kb < nk) return;
+    c_kb = 0;
+    const int j = c_tile++;
 
     // ---------------------------------------------------------------- epilogue
     int mb, nb;
@@ -346,9 +373,16 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
               const int32_t uv = value16(tm, 1, 4 * b + r, nblk + 32 + jl);
               v[r] = rs_sat_f64((double)g.aux_tab[gv + 32768] * (double)uv, g.sh2, lo, hi);
             }
-            const size_t o = (size_t)m * (g.N / 2) + jg + 4 * b;
-            if (g.bits2 == 16) *(uint2*)((int16_t*)g.out + o) = make_uint2(pack16(v[0], v[1]), pack16(v[2], v[3]));
-            else *(int4*)((int32_t*)g.out + o) = make_int4(v[0], v[1], v[2], v[3]);
+            // gated limb planes [bits2 / 8][M][N / 2]
+            const size_t o = (size_t)m * (g.N / 2) + jg + 4 * b, pl = (size_t)g.M * (g.N / 2);
+            uint8_t* ob = (uint8_t*)g.out + o;
+            if (g.bits2 == 16) {
+              *(uint32_t*)ob = limb_word(v, 0, 2);
+              *(uint32_t*)(ob + pl) = limb_word(v, 1, 2);
+            } else {
+#pragma unroll
+              for (int l = 0; l < 4; ++l) *(uint32_t*)(ob + l * pl) = limb_word(v, l, 4);
+            }
           }
         }
       } else {   // EPI_QKV: heads 0..8 q and 9..11 k get RoPE, 12..14 v are stored as they are
@@ -391,8 +425,8 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
         for (int l = 0; l < AW; ++l) acc[a][b][l] = v16i{};
   };
   for (int st = 0; st < nsteps; st += 2) {
-    step(std::integral_constant<int, 0>{}, st);
-    if (st + 1 < nsteps) step(std::integral_constant<int, 1>{}, st + 1);
+    step(I0{}, st);
+    if (st + 1 < nsteps) step(I1{}, st + 1);
   }
 }
 
@@ -415,6 +449,21 @@ hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
   const int per_xcd = std::min((nT + 7) / 8, std::max(1, 2 * device_cus() / 8));
   hipLaunchKernelGGL((gemm_kernel<AW, EPI>), dim3(8 * per_xcd), dim3(C::kThreads), 0, s, a);
   return hipGetLastError();
+}
+
+template <int W>
+__global__ __launch_bounds__(256) void split_kernel(const void* a, size_t n, uint8_t* planes) {
+  const size_t i = ((size_t)blockIdx.x * 256 + threadIdx.x) * 4;   // 4 consecutive elements
+  if (i >= n) return;
+  int32_t v[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = i + e < n ? (W == 2 ? ((const int16_t*)a)[i + e] : ((const int32_t*)a)[i + e]) : 0;
+#pragma unroll
+  for (int l = 0; l < W; ++l) {
+    const uint32_t w = limb_word(v, l, W);
+    if (i + 4 <= n) *(uint32_t*)(planes + l * n + i) = w;
+    else for (size_t e = 0; i + e < n; ++e) planes[l * n + i + e] = (uint8_t)(w >> (8 * e));
+  }
 }
 
 __global__ __launch_bounds__(256) void coef_kernel(const int32_t* mult, const int32_t* shift, const int32_t* wsum,
@@ -459,7 +508,7 @@ __global__ __launch_bounds__(256) void embed_kernel(const int64_t* ids, int M, c
 // One wave per row; lane j holds elements j, j+64, ..., j+512.
 template <int OB>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const int32_t* x, int M, const int32_t* gain,
-                                                      int sh_out, int bits_out, void* out) {
+                                                      int sh_out, int bits_out, uint8_t* planes, void* plain) {
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
   if (row >= M) return;
   const int32_t* xr = x + (size_t)row * kD;
@@ -476,13 +525,21 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const int32_t* x, int M, c
     A += __shfl_xor(A, o); B += __shfl_xor(B, o); Cs += __shfl_xor(Cs, o);
   }
   const int64_t U = norm_U(norm_total(A, B, Cs));
+  const size_t pl = (size_t)M * kD;
 #pragma unroll
   for (int j = 0; j < 9; ++j) {
     const int c = lane + 64 * j;
+    const size_t e = (size_t)row * kD + c;
     const int64_t z = rs((int64_t)v[j] * U, 16);
-    const int64_t o = sat(rs(z * gain[c] * 3, sh_out), bits_out);
-    if constexpr (OB == 2) ((int16_t*)out)[(size_t)row * kD + c] = (int16_t)o;
-    else ((int32_t*)out)[(size_t)row * kD + c] = (int32_t)o;
+    const int32_t o = (int32_t)sat(rs(z * gain[c] * 3, sh_out), bits_out);
+    if (planes) {
+#pragma unroll
+      for (int l = 0; l < OB; ++l) planes[l * pl + e] = (uint8_t)limb_byte(o, l, OB);
+    }
+    if (plain) {
+      if constexpr (OB == 2) ((int16_t*)plain)[e] = (int16_t)o;
+      else ((int32_t*)plain)[e] = o;
+    }
   }
 }
 
@@ -506,7 +563,7 @@ __global__ __launch_bounds__(256) void rope_kernel(int16_t* qkv, int M, const in
 // ------------------------------------------------------------------------------ silu gate
 template <int OB>
 __global__ __launch_bounds__(256) void silu_kernel(const int16_t* gu, int M, const int32_t* silu,
-                                                   int sh, int bits, void* gated) {
+                                                   int sh, int bits, uint8_t* planes, void* plain) {
   const size_t t = (size_t)blockIdx.x * 256 + threadIdx.x;
   if (t >= (size_t)M * kDFF) return;
   const size_t row = t / kDFF, j = t % kDFF;
@@ -514,9 +571,15 @@ __global__ __launch_bounds__(256) void silu_kernel(const int16_t* gu, int M, con
   const size_t gi = row * (2 * kDFF) + 64 * (j / 32) + j % 32;
   const int g = gu[gi];
   const int64_t u = gu[gi + 32];
-  const int64_t o = sat(rs((int64_t)silu[g + 32768] * u, sh), bits);
-  if constexpr (OB == 2) ((int16_t*)gated)[t] = (int16_t)o;
-  else ((int32_t*)gated)[t] = (int32_t)o;
+  const int32_t o = (int32_t)sat(rs((int64_t)silu[g + 32768] * u, sh), bits);
+  if (planes) {
+#pragma unroll
+    for (int l = 0; l < OB; ++l) planes[l * (size_t)M * kDFF + t] = (uint8_t)limb_byte(o, l, OB);
+  }
+  if (plain) {
+    if constexpr (OB == 2) ((int16_t*)plain)[t] = (int16_t)o;
+    else ((int32_t*)plain)[t] = o;
+  }
 }
 
 // ------------------------------------------------------------------------------ attention
@@ -714,14 +777,23 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   const size_t orow = (size_t)(s0 + qi) * kD + hh * 64;
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) {
+    int32_t cvals[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int d = dt * 16 + 4 * gq + r;
       const int64_t acc = (int64_t)C24[dt][r] * (1LL << 24) + (int64_t)C16[dt][r] * 65536 +
                           (int64_t)C8[dt][r] * 256 + C0[dt][r] + 32896 * cv[d] + 128 * SP;
-      const int64_t o = sat(rs(acc, a.sh_ctx), a.bits_c);
-      if constexpr (OB == 2) ((int16_t*)a.ctx)[orow + d] = (int16_t)o;
-      else ((int32_t*)a.ctx)[orow + d] = (int32_t)o;
+      cvals[r] = (int32_t)sat(rs(acc, a.sh_ctx), a.bits_c);
+    }
+    const int d0 = dt * 16 + 4 * gq;
+    if (a.ctx_planes) {
+      const size_t pl = (size_t)a.M * kD;
+#pragma unroll
+      for (int l = 0; l < OB; ++l) *(uint32_t*)(a.ctx_planes + l * pl + orow + d0) = limb_word(cvals, l, OB);
+    }
+    if (a.ctx) {
+      if constexpr (OB == 2) *(uint2*)((int16_t*)a.ctx + orow + d0) = make_uint2(pack16(cvals[0], cvals[1]), pack16(cvals[2], cvals[3]));
+      else *(int4*)((int32_t*)a.ctx + orow + d0) = make_int4(cvals[0], cvals[1], cvals[2], cvals[3]);
     }
   }
 }
@@ -767,11 +839,18 @@ hipError_t embed(const int64_t* ids, int M, const int8_t* emb_q, const int32_t* 
   return hipGetLastError();
 }
 
-hipError_t rmsnorm(const int32_t* x, int M, const int32_t* gain, int sh_out, int bits_out, void* out,
-                   int out_bytes, hipStream_t s) {
+hipError_t rmsnorm(const int32_t* x, int M, const int32_t* gain, int sh_out, int bits_out, uint8_t* planes,
+                   void* plain, hipStream_t s) {
   dim3 grid((M + 3) / 4);
-  if (out_bytes == 2) hipLaunchKernelGGL(rmsnorm_kernel<2>, grid, dim3(256), 0, s, x, M, gain, sh_out, bits_out, out);
-  else hipLaunchKernelGGL(rmsnorm_kernel<4>, grid, dim3(256), 0, s, x, M, gain, sh_out, bits_out, out);
+  if (bits_out == 16) hipLaunchKernelGGL(rmsnorm_kernel<2>, grid, dim3(256), 0, s, x, M, gain, sh_out, bits_out, planes, plain);
+  else hipLaunchKernelGGL(rmsnorm_kernel<4>, grid, dim3(256), 0, s, x, M, gain, sh_out, bits_out, planes, plain);
+  return hipGetLastError();
+}
+
+hipError_t split_limbs(const void* a, int a_bytes, size_t n, uint8_t* planes, hipStream_t s) {
+  dim3 grid((unsigned)((n / 4 + 256) / 256));
+  if (a_bytes == 2) hipLaunchKernelGGL(split_kernel<2>, grid, dim3(256), 0, s, a, n, planes);
+  else hipLaunchKernelGGL(split_kernel<4>, grid, dim3(256), 0, s, a, n, planes);
   return hipGetLastError();
 }
 
@@ -782,18 +861,18 @@ hipError_t rope(int16_t* qkv, int M, const int32_t* pos, const int32_t* cosT, co
   return hipGetLastError();
 }
 
-hipError_t silu_gate(const int16_t* gu, int M, const int32_t* silu, int sh, int bits, void* gated, int out_bytes,
+hipError_t silu_gate(const int16_t* gu, int M, const int32_t* silu, int sh, int bits, uint8_t* planes, void* plain,
                      hipStream_t s) {
   dim3 grid(blocks_for((size_t)M * kDFF));
-  if (out_bytes == 2) hipLaunchKernelGGL(silu_kernel<2>, grid, dim3(256), 0, s, gu, M, silu, sh, bits, gated);
-  else hipLaunchKernelGGL(silu_kernel<4>, grid, dim3(256), 0, s, gu, M, silu, sh, bits, gated);
+  if (bits == 16) hipLaunchKernelGGL(silu_kernel<2>, grid, dim3(256), 0, s, gu, M, silu, sh, bits, planes, plain);
+  else hipLaunchKernelGGL(silu_kernel<4>, grid, dim3(256), 0, s, gu, M, silu, sh, bits, planes, plain);
   return hipGetLastError();
 }
 
-hipError_t attention(const AttnArgs& a, int out_bytes, hipStream_t s) {
+hipError_t attention(const AttnArgs& a, hipStream_t s) {
   if (a.B <= 0 || a.max_T <= 0) return hipSuccess;
   dim3 grid((a.max_T + 63) / 64, kNH, a.B);
-  if (out_bytes == 2) hipLaunchKernelGGL(attn_kernel<2>, grid, dim3(256), 0, s, a);
+  if (a.bits_c == 16) hipLaunchKernelGGL(attn_kernel<2>, grid, dim3(256), 0, s, a);
   else hipLaunchKernelGGL(attn_kernel<4>, grid, dim3(256), 0, s, a);
   return hipGetLastError();
 }

@@ -57,12 +57,10 @@ __device__ __forceinline__ uint32_t limb_word(const int32_t* v, int l, int W) {
 // ------------------------------------------------------------------------------ GEMM
 // Persistent workgroups of 4 waves (two per CU, so one's epilogue overlaps the other's MFMA loop)
 // sweep BM x 128 output tiles (BM = 128 for 2-limb activations, 64 for 4-limb) in a flat
-// (tile, K block of 64) loop with two LDS stages fed through registers loaded two steps ahead.
-// v_mfma_i32_32x32x32_i8 runs with the weights as the A operand and the activations as the B
-// operand, D[n][m] = sum_k W[n,k] a[m,k]; it sustains about twice the int8 rate of the 16x16x64
-// form on gfx950.  The order of the weight rows inside a wave's 64-column block is free, so it is
-// chosen per epilogue (col_perm): 32 consecutive output columns per lane (contiguous stores), or
-// the (gate j, up j) and RoPE (d, d+32) pairs in one lane.
+// (tile, K block of 64) loop.  Activation limb planes pass through two LDS stages; each wave
+// loads its weight fragments straight into registers (the weights are L2-resident), both two
+// steps ahead.  v_mfma_i32_32x32x32_i8 sustains about twice the int8 rate of the 16x16x64 form
+// on gfx950.
 //
 // Epilogue arithmetic for 2-limb inputs runs in float64 and is exact: with P1, P0 the limb
 // partial sums (|P| < 2^25 for K <= 1536) and |m| <= 2^14,
@@ -89,26 +87,15 @@ __device__ __forceinline__ int32_t rs_sat_f64(double x, int sh, double lo, doubl
   return rne_i32(fmin(fmax(y, lo), hi));
 }
 
-enum Perm { PERM_CONTIG = 0, PERM_PAIR = 1 };
-
 typedef int v16i __attribute__((ext_vector_type(16)));
 __device__ __forceinline__ v16i mfma32(v4i a, v4i b, v16i c) {
   return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
 }
 
-// 32x32 output tile of v_mfma_i32_32x32x32_i8, lane = 32 h + c, register j = 4 b + r: row
-// i = 8 b + 4 h + r, column c.  The weights are the A operand, so i indexes a weight row of the
-// tile.  Column of a wave's 64-column block held at (n-tile tn, tile row i):
-//   PERM_CONTIG: lane h holds block columns 32h .. 32h+31 (contiguous stores)
-//   PERM_PAIR:   lane h holds 16h .. 16h+15 (tn = 0) and 32+16h .. 32+16h+15 (tn = 1), i.e. the
-//                (gate j, up j) and RoPE (d, d + 32) pairs
-template <int P>
-__device__ __forceinline__ int col_perm(int tn, int i) {
-  const int b = i >> 3, h = (i >> 2) & 1, r = i & 3;
-  if constexpr (P == PERM_CONTIG) return 32 * h + 16 * tn + 4 * b + r;
-  else return 32 * tn + 16 * h + 4 * b + r;
-}
-
+// v_mfma_i32_32x32x32_i8 with the activations as the A operand and the weights as the B operand:
+// D[m][n] = sum_k a[m,k] W[n,k].  Lane = 32 h + c, register j = 4 b + r holds row
+// i = 8 b + 4 h + r, column c of the 32x32 tile: the 32 lanes of a half-wave hold 32
+// consecutive columns of one row, so every epilogue store is a contiguous run.
 template <int AW>
 struct GemmCfg {
   static constexpr int kThreads = 256;                   // 4 waves; two workgroups share a CU
@@ -116,14 +103,10 @@ struct GemmCfg {
   static constexpr int WM = BM / 2, WN = 64;             // 2 x 2 waves
   static constexpr int TM = WM / 32, TN = 2;             // 32x32 tiles per wave
   static constexpr int kPlane = BM * kLdsRow;
-  static constexpr int kABytes = AW * kPlane;
-  static constexpr int kStage = kABytes + BN * kLdsRow;
+  static constexpr int kStage = AW * kPlane;              // activation limb planes only
   static constexpr int kAChunks = AW * BM * 4 / kThreads;   // 16-byte global loads per thread
-  static constexpr int kBChunks = BN * 4 / kThreads;
-  static_assert(kAChunks * kThreads == BM * 4 * AW && kBChunks * kThreads == BN * 4, "chunk split");
+  static_assert(kAChunks * kThreads == AW * BM * 4, "chunk split");
 };
-
-template <int EPI> struct EpiPerm { static constexpr int P = (EPI == EPI_SILU || EPI == EPI_QKV) ? PERM_PAIR : PERM_CONTIG; };
 
 // Tiles in grouped order: 8 row blocks x all column blocks per group.  Each XCD (= blockIdx % 8,
 // the hardware's round-robin dispatch) owns a contiguous range of that order, and the persistent
@@ -141,7 +124,6 @@ __device__ __forceinline__ uint32_t pack16(int32_t a, int32_t b) { return (uint3
 template <int AW, int EPI>
 __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
   using C = GemmCfg<AW>;
-  constexpr int P = EpiPerm<EPI>::P;
   __shared__ __attribute__((aligned(16))) uint8_t smem[2 * C::kStage];
   const int nMB = (g.M + C::BM - 1) / C::BM, nNB = (g.N + C::BN - 1) / C::BN, nT = nMB * nNB;
   // this workgroup's tiles: v = v0, v0 + stride, ... < vend
@@ -153,47 +135,50 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
+  const int fc = lane & 31, fh = lane >> 5;
   const uint8_t* Ab = (const uint8_t*)g.A;
 
-  // Load cursor: the tile and K block of the next step to load, with this thread's source
-  // pointers for that tile (advanced incrementally; divisions happen once per tile).
+  // Load cursor: tile and K block of the next step to load, with this thread's source pointers
+  // for that tile (advanced incrementally; divisions happen once per tile).  Rows past M and
+  // columns past N read row M - 1 / N - 1; their results are never stored.
   int l_tile = 0, l_kb = 0;
   const uint8_t* a_src[C::kAChunks];
-  const int8_t* w_src[C::kBChunks];
+  const int8_t* w_src[C::TN];
   auto set_load_tile = [&](int j) {
     int mb, nb;
     tile_coords(v0 + j * nwg_x, nMB, nNB, mb, nb);
     const int m0 = mb * C::BM, n0 = nb * C::BN;
 #pragma unroll
     for (int i = 0; i < C::kAChunks; ++i) {
-      // chunk q: limb plane l, row, 16-byte chunk c; rows past M read row M - 1 (never stored)
+      // chunk q: limb plane l, row, 16-byte chunk c
       const int q = tid + C::kThreads * i, l = q / (4 * C::BM), row = (q >> 2) % C::BM, c = q & 3;
       const int m = min(m0 + row, g.M - 1);
       a_src[i] = Ab + (size_t)l * g.a_plane + (size_t)m * g.K + c * 16;
     }
 #pragma unroll
-    for (int i = 0; i < C::kBChunks; ++i) {
-      // LDS weight row rho holds global row n0 + 64 (rho / 64) + col_perm(tn, i); rows past N read
-      // row N - 1 (their columns are never stored)
-      const int rho = (tid + C::kThreads * i) >> 2;
-      const int wrow = min(n0 + (rho & 64) + col_perm<P>((rho >> 5) & 1, rho & 31), g.N - 1);
-      w_src[i] = g.W + (size_t)wrow * g.K + (tid & 3) * 16;
+    for (int tn = 0; tn < C::TN; ++tn) {
+      // this lane's B fragment: weight row n0 + 64 wn + 32 tn + c, K bytes 16 h of each 32-step
+      const int n = min(n0 + wn * C::WN + 32 * tn + fc, g.N - 1);
+      w_src[tn] = g.W + (size_t)n * g.K + 16 * fh;
     }
   };
-  u32x4 areg[2][C::kAChunks], breg[2][C::kBChunks];
+  u32x4 areg[2][C::kAChunks];
+  v4i wreg[2][C::TN][2];
   auto load = [&](auto SET) {   // the step at the cursor, into register set SET (compile time)
     constexpr int set = decltype(SET)::value;
     const int kw = l_kb * kBK;
 #pragma unroll
     for (int i = 0; i < C::kAChunks; ++i) areg[set][i] = *(const u32x4*)(a_src[i] + kw);
 #pragma unroll
-    for (int i = 0; i < C::kBChunks; ++i) breg[set][i] = *(const u32x4*)(w_src[i] + kw);
+    for (int tn = 0; tn < C::TN; ++tn)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) wreg[set][tn][ks] = *(const v4i*)(w_src[tn] + kw + 32 * ks);
     if (++l_kb == nk) {
       l_kb = 0;
       if (++l_tile < ntiles) set_load_tile(l_tile);
     }
   };
-  auto store = [&](auto SET) {   // register set SET into LDS stage SET
+  auto store = [&](auto SET) {   // activation register set SET into LDS stage SET
     constexpr int set = decltype(SET)::value;
     uint8_t* base = smem + set * C::kStage;
 #pragma unroll
@@ -201,9 +186,6 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
       const int q = tid + C::kThreads * i, l = q / (4 * C::BM), row = (q >> 2) % C::BM, c = q & 3;
       *(u32x4*)(base + l * C::kPlane + row * kLdsRow + c * 16) = areg[set][i];
     }
-#pragma unroll
-    for (int i = 0; i < C::kBChunks; ++i)
-      *(u32x4*)(base + C::kABytes + ((tid + C::kThreads * i) >> 2) * kLdsRow + (tid & 3) * 16) = breg[set][i];
   };
 
   v16i acc[C::TM][C::TN][AW];
@@ -214,8 +196,8 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
 #pragma unroll
       for (int l = 0; l < AW; ++l) acc[a][b][l] = v16i{};
 
-  // Step s computes from LDS stage s % 2; its global data was loaded two steps earlier into
-  // register set s % 2 and stored to LDS during step s - 1.
+  // Step s computes from LDS stage s % 2 and weight register set s % 2; both were loaded two
+  // steps earlier, the activations stored to LDS during step s - 1.
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
   set_load_tile(0);
@@ -223,28 +205,25 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
   if (nsteps > 1) load(I1{});
   store(I0{});
   __syncthreads();
-  const int fc = lane & 31, fh = lane >> 5;
   int c_tile = 0, c_kb = 0;   // tile and K block being computed
-  // one step; CUR = st % 2 is a compile-time constant so the register sets stay in registers
   auto step = [&](auto CUR, int st) {
     constexpr int cur = decltype(CUR)::value;
     using NXT = std::integral_constant<int, cur ^ 1>;
+    v4i wf[C::TN][2];
+#pragma unroll
+    for (int tn = 0; tn < C::TN; ++tn) { wf[tn][0] = wreg[cur][tn][0]; wf[tn][1] = wreg[cur][tn][1]; }
     if (st + 2 < nsteps) load(CUR);
     const uint8_t* base = smem + cur * C::kStage;
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       const int fk = 32 * ks + 16 * fh;
-      v4i wf[C::TN];
-#pragma unroll
-      for (int tn = 0; tn < C::TN; ++tn)
-        wf[tn] = *(const v4i*)(base + C::kABytes + (wn * C::WN + tn * 32 + fc) * kLdsRow + fk);
 #pragma unroll
       for (int tm = 0; tm < C::TM; ++tm) {
 #pragma unroll
         for (int l = 0; l < AW; ++l) {
           const v4i af = *(const v4i*)(base + l * C::kPlane + (wm * C::WM + tm * 32 + fc) * kLdsRow + fk);
 #pragma unroll
-          for (int tn = 0; tn < C::TN; ++tn) acc[tm][tn][l] = mfma32(wf[tn], af, acc[tm][tn][l]);
+          for (int tn = 0; tn < C::TN; ++tn) acc[tm][tn][l] = mfma32(af, wf[tn][ks], acc[tm][tn][l]);
         }
       }
     }
@@ -252,103 +231,79 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
     __syncthreads();
     if (++c_kb < nk) return;
     c_kb = 0;
-    const int j = c_tile++;
+    const int jt = c_tile++;
 
     // ---------------------------------------------------------------- epilogue
     int mb, nb;
-    tile_coords(v0 + j * nwg_x, nMB, nNB, mb, nb);
-    const int m0 = mb * C::BM, n0 = nb * C::BN;
-    const int nblk = n0 + wn * C::WN;                   // first column of this wave's block
-    int mrow[C::TM];
-#pragma unroll
-    for (int tm = 0; tm < C::TM; ++tm) mrow[tm] = m0 + wm * C::WM + tm * 32 + fc;
+    tile_coords(v0 + jt * nwg_x, nMB, nNB, mb, nb);
+    const int mbase = mb * C::BM + wm * C::WM + 4 * fh;   // row of (tm, j) = mbase + 32 tm + 8 (j/4) + (j%4)
+    const int nblk = nb * C::BN + wn * C::WN;              // column of (tn) = nblk + 32 tn + fc
     const int64_t bias = limb_bias(AW);
-    // exact int64 accumulator of register e of tile (tm, tn)
     auto acc64 = [&](int tm, int tn, int e, int32_t ws) -> int64_t {
       int64_t a = bias * (int64_t)ws;
 #pragma unroll
       for (int l = 0; l < AW; ++l) a += (int64_t)acc[tm][tn][l][e] * ((int64_t)1 << (8 * l));
       return a;
     };
+    auto row_of = [&](int tm, int e) { return mbase + 32 * tm + 8 * (e >> 2) + (e & 3); };
 
-    if constexpr (P == PERM_CONTIG) {
-      // lane holds block columns 32 fh + 16 tn + 4 b + r: groups of 4 consecutive columns
+    if constexpr (EPI == EPI_I64 || EPI == EPI_REQ16 || EPI == EPI_REQ32 || EPI == EPI_RESID || EPI == EPI_LOGITS) {
       const double lo = EPI == EPI_REQ16 || EPI == EPI_REQ32 ? -ldexp(1.0, g.sat_bits - 1) : 0.0;
       const double hi = EPI == EPI_REQ16 || EPI == EPI_REQ32 ? ldexp(1.0, g.sat_bits - 1) - 1.0 : 0.0;
 #pragma unroll
-      for (int tn = 0; tn < C::TN; ++tn)
+      for (int tn = 0; tn < C::TN; ++tn) {
+        const int n = nblk + 32 * tn + fc;
+        if (n >= g.N) continue;
+        const int32_t ws = (AW == 4 || EPI == EPI_I64) ? g.wsum[n] : 0;
+        int32_t mu = 0, sh = 1;
+        double2 k = make_double2(0.0, 0.0);
+        if constexpr (AW == 4 && EPI != EPI_I64) { mu = g.mult[n]; sh = g.shift[n]; }
+        if constexpr (AW == 2 && EPI != EPI_I64) k = g.coef[n];
+        bool bad = false;
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
-          const int nc = nblk + 32 * fh + 16 * tn + 4 * b;    // columns nc .. nc+3
-          if (nc >= g.N) continue;                              // N is a multiple of 4
-          int4 ws4 = make_int4(0, 0, 0, 0), mu4 = make_int4(0, 0, 0, 0), sh4 = make_int4(1, 1, 1, 1);
-          double2 k[4];
-          if constexpr (AW == 4 || EPI == EPI_I64) ws4 = *(const int4*)(g.wsum + nc);
-          if constexpr (AW == 4 && EPI != EPI_I64) { mu4 = *(const int4*)(g.mult + nc); sh4 = *(const int4*)(g.shift + nc); }
-          if constexpr (AW == 2 && EPI != EPI_I64) {
+        for (int tm = 0; tm < C::TM; ++tm)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) k[r] = g.coef[nc + r];
-          }
-          const int wsv[4] = {ws4.x, ws4.y, ws4.z, ws4.w}, muv[4] = {mu4.x, mu4.y, mu4.z, mu4.w},
-                    shv[4] = {sh4.x, sh4.y, sh4.z, sh4.w};
-#pragma unroll
-          for (int tm = 0; tm < C::TM; ++tm) {
-            const int m = mrow[tm];
+          for (int e = 0; e < 16; ++e) {
+            const int m = row_of(tm, e);
             if (m >= g.M) continue;
-            const size_t o = (size_t)m * g.N + nc;
+            const size_t o = (size_t)m * g.N + n;
             if constexpr (EPI == EPI_I64) {
-              int64_t* op = (int64_t*)g.out + o;
-              *(longlong2*)op = make_longlong2(acc64(tm, tn, 4 * b, wsv[0]), acc64(tm, tn, 4 * b + 1, wsv[1]));
-              *(longlong2*)(op + 2) = make_longlong2(acc64(tm, tn, 4 * b + 2, wsv[2]), acc64(tm, tn, 4 * b + 3, wsv[3]));
+              ((int64_t*)g.out)[o] = acc64(tm, tn, e, ws);
               continue;
             }
-            // t2[r] = RS(acc * m, sh) as an exact integer-valued double (2 limbs) or int64 (4 limbs)
-            double y[4];
-            int64_t v[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              if constexpr (AW == 2) y[r] = req2(acc[tm][tn][1][4 * b + r], acc[tm][tn][0][4 * b + r], k[r]);
-              else v[r] = rs(acc64(tm, tn, 4 * b + r, wsv[r]) * muv[r], shv[r]);
-            }
+            // RS(acc * m, sh): exact integer-valued double + 2^-(sh+1) offset (2 limbs) or int64 (4 limbs)
+            double y = 0.0;
+            int64_t v = 0;
+            if constexpr (AW == 2) y = req2(acc[tm][tn][1][e], acc[tm][tn][0][e], k);
+            else v = rs(acc64(tm, tn, e, ws) * mu, sh);
             if constexpr (EPI == EPI_REQ16 || EPI == EPI_REQ32) {
-              int32_t q[4];
-#pragma unroll
-              for (int r = 0; r < 4; ++r)
-                q[r] = AW == 2 ? rne_i32(fmin(fmax(y[r], lo), hi)) : (int32_t)sat(v[r], g.sat_bits);
-              if constexpr (EPI == EPI_REQ16) *(uint2*)((int16_t*)g.out + o) = make_uint2(pack16(q[0], q[1]), pack16(q[2], q[3]));
-              else *(int4*)((int32_t*)g.out + o) = make_int4(q[0], q[1], q[2], q[3]);
+              const int32_t q = AW == 2 ? rne_i32(fmin(fmax(y, lo), hi)) : (int32_t)sat(v, g.sat_bits);
+              if constexpr (EPI == EPI_REQ16) ((int16_t*)g.out)[o] = (int16_t)q;
+              else ((int32_t*)g.out)[o] = q;
             } else if constexpr (EPI == EPI_RESID) {
-              int4* xp = (int4*)((int32_t*)g.out + o);
-              const int4 x = *xp;
-              const int32_t xv[4] = {x.x, x.y, x.z, x.w};
-              int32_t q[4];
-#pragma unroll
-              for (int r = 0; r < 4; ++r)
-                q[r] = AW == 2 ? rne_i32(fmin(fmax(rint(y[r]) + (double)xv[r], -2147483648.0), 2147483647.0))
-                               : (int32_t)clamp_bits32((int64_t)xv[r] + v[r]);
-              *xp = make_int4(q[0], q[1], q[2], q[3]);
+              int32_t* xp = (int32_t*)g.out + o;
+              const int32_t x = *xp;
+              *xp = AW == 2 ? rne_i32(fmin(fmax(rint(y) + (double)x, -2147483648.0), 2147483647.0))
+                            : (int32_t)clamp_bits32((int64_t)x + v);
             } else {   // EPI_LOGITS
-              int32_t q[4];
-              bool bad = false;
-#pragma unroll
-              for (int r = 0; r < 4; ++r) {
-                if constexpr (AW == 2) {
-                  const double t2 = rint(y[r]);
-                  bad |= t2 > 2147483647.0 || t2 < -2147483648.0;
-                  q[r] = rne_i32(t2);
-                } else {
-                  bad |= v[r] != (int64_t)(int32_t)v[r];
-                  q[r] = (int32_t)v[r];
-                }
+              if constexpr (AW == 2) {
+                const double t2 = rint(y);
+                bad |= t2 > 2147483647.0 || t2 < -2147483648.0;
+                ((int32_t*)g.out)[o] = rne_i32(t2);
+              } else {
+                bad |= v != (int64_t)(int32_t)v;
+                ((int32_t*)g.out)[o] = (int32_t)v;
               }
-              if (bad) atomicOr(g.flag, 1);
-              *(int4*)((int32_t*)g.out + o) = make_int4(q[0], q[1], q[2], q[3]);
             }
           }
+        if constexpr (EPI == EPI_LOGITS) {
+          if (bad) atomicOr(g.flag, 1);
         }
+      }
     } else if (nblk < g.N) {
-      // PERM_PAIR: lane holds block columns jl = 16 fh + 4 b + r (tn = 0) and jl + 32 (tn = 1):
-      // (gate j, up j) for EPI_SILU, (d, d + 32) of one head for EPI_QKV
+      // columns c (tn = 0) and 32 + c (tn = 1) of the wave's 64-column block: (gate j, up j) for
+      // EPI_SILU (weight rows stacked as [gate 32 | up 32] blocks), (d, d + 32) of one head for EPI_QKV
+      const int nc = nblk + fc;
       auto value16 = [&](int tm, int tn, int e, int n) -> int32_t {   // SAT16(RS(acc * m, sh)) of column n
         if constexpr (AW == 2) {
           return rne_i32(fmin(fmax(req2(acc[tm][tn][1][e], acc[tm][tn][0][e], g.coef[n]), -32768.0), 32767.0));
@@ -358,63 +313,47 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
       };
       if constexpr (EPI == EPI_SILU) {
         const double lo = -ldexp(1.0, g.bits2 - 1), hi = ldexp(1.0, g.bits2 - 1) - 1.0;
-        const int jg = (nblk >> 6) * 32 + 16 * fh;          // gated column of jl = 16 fh
+        const int jg = (nblk >> 6) * 32 + fc;               // gated column
+        const size_t pl = (size_t)g.M * (g.N / 2);
 #pragma unroll
-        for (int tm = 0; tm < C::TM; ++tm) {
-          const int m = mrow[tm];
-          if (m >= g.M) continue;
+        for (int tm = 0; tm < C::TM; ++tm)
 #pragma unroll
-          for (int b = 0; b < 4; ++b) {
-            int32_t v[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const int jl = 16 * fh + 4 * b + r;
-              const int32_t gv = value16(tm, 0, 4 * b + r, nblk + jl);
-              const int32_t uv = value16(tm, 1, 4 * b + r, nblk + 32 + jl);
-              v[r] = rs_sat_f64((double)g.aux_tab[gv + 32768] * (double)uv, g.sh2, lo, hi);
-            }
+          for (int e = 0; e < 16; ++e) {
+            const int m = row_of(tm, e);
+            if (m >= g.M) continue;
+            const int32_t gv = value16(tm, 0, e, nc), uv = value16(tm, 1, e, nc + 32);
+            const int32_t v = rs_sat_f64((double)g.aux_tab[gv + 32768] * (double)uv, g.sh2, lo, hi);
             // gated limb planes [bits2 / 8][M][N / 2]
-            const size_t o = (size_t)m * (g.N / 2) + jg + 4 * b, pl = (size_t)g.M * (g.N / 2);
-            uint8_t* ob = (uint8_t*)g.out + o;
+            uint8_t* ob = (uint8_t*)g.out + (size_t)m * (g.N / 2) + jg;
             if (g.bits2 == 16) {
-              *(uint32_t*)ob = limb_word(v, 0, 2);
-              *(uint32_t*)(ob + pl) = limb_word(v, 1, 2);
+              ob[0] = (uint8_t)limb_byte(v, 0, 2);
+              ob[pl] = (uint8_t)limb_byte(v, 1, 2);
             } else {
 #pragma unroll
-              for (int l = 0; l < 4; ++l) *(uint32_t*)(ob + l * pl) = limb_word(v, l, 4);
+              for (int l = 0; l < 4; ++l) ob[l * pl] = (uint8_t)limb_byte(v, l, 4);
             }
           }
-        }
       } else {   // EPI_QKV: heads 0..8 q and 9..11 k get RoPE, 12..14 v are stored as they are
         const int head = nblk >> 6;
         const int shr = head < 9 ? g.sh_q : g.sh_k;
 #pragma unroll
-        for (int tm = 0; tm < C::TM; ++tm) {
-          const int m = mrow[tm];
-          if (m >= g.M) continue;
-          const int ps = head < 12 ? g.pos[m] : 0;
-          int16_t* op = (int16_t*)g.out + (size_t)m * g.N + nblk + 16 * fh;
+        for (int tm = 0; tm < C::TM; ++tm)
 #pragma unroll
-          for (int b = 0; b < 4; ++b) {
-            int32_t lo4[4], hi4[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const int d = 16 * fh + 4 * b + r;
-              const int32_t a1 = value16(tm, 0, 4 * b + r, nblk + d), a2 = value16(tm, 1, 4 * b + r, nblk + 32 + d);
-              if (head < 12) {
-                const double c = (double)g.cosT[ps * 32 + d], sn = (double)g.sinT[ps * 32 + d];
-                const double o1 = fma((double)a1, c, -(double)a2 * sn), o2 = fma((double)a2, c, (double)a1 * sn);
-                lo4[r] = rs_sat_f64(o1, shr, -32768.0, 32767.0);
-                hi4[r] = rs_sat_f64(o2, shr, -32768.0, 32767.0);
-              } else {
-                lo4[r] = a1;
-                hi4[r] = a2;
-              }
+          for (int e = 0; e < 16; ++e) {
+            const int m = row_of(tm, e);
+            if (m >= g.M) continue;
+            const int32_t a1 = value16(tm, 0, e, nc), a2 = value16(tm, 1, e, nc + 32);
+            int32_t o1 = a1, o2 = a2;
+            if (head < 12) {
+              const int ps = g.pos[m];
+              const double c = (double)g.cosT[ps * 32 + fc], sn = (double)g.sinT[ps * 32 + fc];
+              o1 = rs_sat_f64(fma((double)a1, c, -(double)a2 * sn), shr, -32768.0, 32767.0);
+              o2 = rs_sat_f64(fma((double)a2, c, (double)a1 * sn), shr, -32768.0, 32767.0);
             }
-            *(uint2*)(op + 4 * b) = make_uint2(pack16(lo4[0], lo4[1]), pack16(lo4[2], lo4[3]));
-            *(uint2*)(op + 32 + 4 * b) = make_uint2(pack16(hi4[0], hi4[1]), pack16(hi4[2], hi4[3]));
+            int16_t* op = (int16_t*)g.out + (size_t)m * g.N + nc;
+            op[0] = (int16_t)o1;
+            op[32] = (int16_t)o2;
           }
-        }
       }
     }
 #pragma unroll

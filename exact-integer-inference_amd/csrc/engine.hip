@@ -725,7 +725,7 @@ extern "C" int eii_weight_colsum(const int8_t* W, int N, int K, int32_t* wsum, v
 static int check_gemm_args(const void* A, int a_bits, const int8_t* W, int M, int N, int K) {
   if (!A || !W || M <= 0 || N <= 0 || K <= 0) return fail(EII_E_ARG, "bad gemm arguments");
   if (a_bits != 16 && a_bits != 32) return fail(EII_E_ARG, "a_bits must be 16 or 32");
-  if (K % 64) return fail(EII_E_ARG, "K must be a multiple of 64");
+  if (K != 64 && K != 128 && K != 576 && K != 1536) return fail(EII_E_ARG, "K must be 64, 128, 576 or 1536");
   if (K > 65536) return fail(EII_E_BOUND, "K above 65536 could overflow a limb partial sum");
   return EII_OK;
 }

@@ -121,9 +121,10 @@ __device__ __forceinline__ void tile_coords(int v, int nMB, int nNB, int& mb, in
 
 __device__ __forceinline__ uint32_t pack16(int32_t a, int32_t b) { return (uint32_t)(a & 0xFFFF) | ((uint32_t)b << 16); }
 
-template <int AW, int EPI>
+template <int AW, int EPI, int NK>
 __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
   using C = GemmCfg<AW>;
+  static_assert(NK >= 1, "at least one K block");
   __shared__ __attribute__((aligned(16))) uint8_t smem[2 * C::kStage];
   const int nMB = (g.M + C::BM - 1) / C::BM, nNB = (g.N + C::BN - 1) / C::BN, nT = nMB * nNB;
   // this workgroup's tiles: v = v0, v0 + stride, ... < vend
@@ -131,7 +132,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
   const int v0 = xcd * per + (blockIdx.x >> 3), vend = min(nT, (xcd + 1) * per);
   if (v0 >= vend) return;
   const int ntiles = (vend - v0 + nwg_x - 1) / nwg_x;
-  const int nk = g.K / kBK, nsteps = ntiles * nk;
+  constexpr int nk = NK;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
@@ -144,7 +145,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
   int l_tile = 0, l_kb = 0;
   const uint8_t* a_src[C::kAChunks];
   const int8_t* w_src[C::TN];
-  auto set_load_tile = [&](int j) {
+  auto set_load_tile = [&](int j) __attribute__((always_inline)) {
     int mb, nb;
     tile_coords(v0 + j * nwg_x, nMB, nNB, mb, nb);
     const int m0 = mb * C::BM, n0 = nb * C::BN;
@@ -164,7 +165,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
   };
   u32x4 areg[2][C::kAChunks];
   v4i wreg[2][C::TN][2];
-  auto load = [&](auto SET) {   // the step at the cursor, into register set SET (compile time)
+  auto load = [&](auto SET) __attribute__((always_inline)) {   // the step at the cursor, into register set SET (compile time)
     constexpr int set = decltype(SET)::value;
     const int kw = l_kb * kBK;
 #pragma unroll
@@ -178,7 +179,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
       if (++l_tile < ntiles) set_load_tile(l_tile);
     }
   };
-  auto store = [&](auto SET) {   // activation register set SET into LDS stage SET
+  auto store = [&](auto SET) __attribute__((always_inline)) {   // activation register set SET into LDS stage SET
     constexpr int set = decltype(SET)::value;
     uint8_t* base = smem + set * C::kStage;
 #pragma unroll
@@ -197,41 +198,43 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
       for (int l = 0; l < AW; ++l) acc[a][b][l] = v16i{};
 
   // Step s computes from LDS stage s % 2 and weight register set s % 2; both were loaded two
-  // steps earlier, the activations stored to LDS during step s - 1.
+  // steps earlier, the activations stored to LDS during step s - 1.  Every tile is unrolled
+  // (two tiles per iteration when NK is odd), so the parity of each step is a compile-time
+  // constant and the code between waits is straight-line.
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
+  const int nsteps = ntiles * nk;
   set_load_tile(0);
   load(I0{});
   if (nsteps > 1) load(I1{});
   store(I0{});
   __syncthreads();
-  int c_tile = 0, c_kb = 0;   // tile and K block being computed
-  auto step = [&](auto CUR, int st) {
+  // step kb of tile jt (cur = parity of the global step); more = a step two ahead exists
+  auto step = [&](auto CUR, int jt, int kb, bool more2, bool more1) __attribute__((always_inline)) {
     constexpr int cur = decltype(CUR)::value;
     using NXT = std::integral_constant<int, cur ^ 1>;
-    v4i wf[C::TN][2];
-#pragma unroll
-    for (int tn = 0; tn < C::TN; ++tn) { wf[tn][0] = wreg[cur][tn][0]; wf[tn][1] = wreg[cur][tn][1]; }
-    if (st + 2 < nsteps) load(CUR);
     const uint8_t* base = smem + cur * C::kStage;
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       const int fk = 32 * ks + 16 * fh;
+      v4i af[C::TM][AW];   // all A fragments of this K step first, so their LDS latencies overlap
 #pragma unroll
-      for (int tm = 0; tm < C::TM; ++tm) {
+      for (int tm = 0; tm < C::TM; ++tm)
 #pragma unroll
-        for (int l = 0; l < AW; ++l) {
-          const v4i af = *(const v4i*)(base + l * C::kPlane + (wm * C::WM + tm * 32 + fc) * kLdsRow + fk);
+        for (int l = 0; l < AW; ++l)
+          af[tm][l] = *(const v4i*)(base + l * C::kPlane + (wm * C::WM + tm * 32 + fc) * kLdsRow + fk);
 #pragma unroll
-          for (int tn = 0; tn < C::TN; ++tn) acc[tm][tn][l] = mfma32(af, wf[tn][ks], acc[tm][tn][l]);
-        }
-      }
+      for (int tm = 0; tm < C::TM; ++tm)
+#pragma unroll
+        for (int l = 0; l < AW; ++l)
+#pragma unroll
+          for (int tn = 0; tn < C::TN; ++tn) acc[tm][tn][l] = mfma32(af[tm][l], wreg[cur][tn][ks], acc[tm][tn][l]);
     }
-    if (st + 1 < nsteps) store(NXT{});
+    // the weight registers of this step are consumed: the prefetch two steps ahead reuses them
+    if (more2) load(CUR);
+    if (more1) store(NXT{});
     __syncthreads();
-    if (++c_kb < nk) return;
-    c_kb = 0;
-    const int jt = c_tile++;
+    if (kb != nk - 1) return;
 
     // ---------------------------------------------------------------- epilogue
     int mb, nb;
@@ -363,9 +366,25 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
 #pragma unroll
         for (int l = 0; l < AW; ++l) acc[a][b][l] = v16i{};
   };
-  for (int st = 0; st < nsteps; st += 2) {
-    step(I0{}, st);
-    if (st + 1 < nsteps) step(I1{}, st + 1);
+  auto tile = [&](auto PAR, int jt) __attribute__((always_inline)) {   // PAR = parity of the tile's first step
+    constexpr int p0 = decltype(PAR)::value;
+#pragma unroll
+    for (int kb = 0; kb < nk; ++kb) {
+      const int st = jt * nk + kb;
+      const bool more1 = st + 1 < nsteps, more2 = st + 2 < nsteps;
+      if ((kb + p0) % 2 == 0) step(I0{}, jt, kb, more2, more1);
+      else step(I1{}, jt, kb, more2, more1);
+    }
+  };
+  if constexpr (nk % 2 == 0) {
+    for (int jt = 0; jt < ntiles; ++jt) tile(I0{}, jt);
+  } else {
+    int jt = 0;
+    for (; jt + 1 < ntiles; jt += 2) {
+      tile(I0{}, jt);
+      tile(I1{}, jt + 1);
+    }
+    if (jt < ntiles) tile(I0{}, jt);
   }
 }
 
@@ -386,7 +405,19 @@ hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
   const int nT = ((a.M + C::BM - 1) / C::BM) * ((a.N + C::BN - 1) / C::BN);
   // two persistent workgroups per CU, a multiple of 8 so every XCD gets the same count
   const int per_xcd = std::min((nT + 7) / 8, std::max(1, 2 * device_cus() / 8));
-  hipLaunchKernelGGL((gemm_kernel<AW, EPI>), dim3(8 * per_xcd), dim3(C::kThreads), 0, s, a);
+  const dim3 grid(8 * per_xcd), block(C::kThreads);
+  // K is a template parameter so each tile's K loop is straight-line code: the model's K
+  // (576, 1536) for every epilogue, and 64, 128 for the operator entry points
+  constexpr bool op = EPI == EPI_I64 || EPI == EPI_REQ16 || EPI == EPI_REQ32;
+  switch (a.K / kBK) {
+    case 9: hipLaunchKernelGGL((gemm_kernel<AW, EPI, 9>), grid, block, 0, s, a); break;
+    case 24: hipLaunchKernelGGL((gemm_kernel<AW, EPI, 24>), grid, block, 0, s, a); break;
+    case 1: if constexpr (op) { hipLaunchKernelGGL((gemm_kernel<AW, EPI, 1>), grid, block, 0, s, a); break; }
+            return hipErrorInvalidValue;
+    case 2: if constexpr (op) { hipLaunchKernelGGL((gemm_kernel<AW, EPI, 2>), grid, block, 0, s, a); break; }
+            return hipErrorInvalidValue;
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 

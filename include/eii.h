@@ -102,7 +102,8 @@ int eii_profile_end(eii_model* m, void* stream, double* ms, int* launches);
 int eii_weight_colsum(const int8_t* W_dev, int N, int K, int32_t* wsum_dev, void* stream);
 
 /* Exact acc_dev int64 [M, N] = A W^T (python/intref.py:58-63 matmul_exact) with A_dev int16
- * (a_bits 16) or int32 (a_bits 32) [M, K], W_dev int8 [N, K], K % 64 == 0. */
+ * (a_bits 16) or int32 (a_bits 32) [M, K], W_dev int8 [N, K]; K in {64, 128, 576, 1536},
+ * N a multiple of 4. */
 int eii_gemm_i8(const void* A_dev, int a_bits, const int8_t* W_dev, int M, int N, int K,
                 int64_t* acc_dev, void* stream);
 /* The same with precomputed row sums (eii_weight_colsum). */

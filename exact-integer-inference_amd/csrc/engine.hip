@@ -94,12 +94,14 @@ struct eii_model {
   int32_t* x = nullptr;            // [M, 576]
   void* h = nullptr;               // [M, 576] up to int32
   int16_t* qkv = nullptr;          // [M, 960]
+  uint8_t* vt = nullptr;           // V^T limb planes (kernels.h vt_bytes)
   void* ctx = nullptr;             // [M, 576] up to int32
   int16_t* gu = nullptr;           // [M, 3072]
   void* gated = nullptr;           // [M, 1536] up to int32
   int32_t* pos = nullptr;          // [M]
   int32_t* seq_off = nullptr;      // [nseq + 1]
   size_t seq_cap = 0;
+  int max_kt = 0;                  // key tiles of the longest-spanning sequence of the batch
   std::vector<int32_t> last_lens;
   int* flags = nullptr;            // [1]: 1 logit overflow, 2 token id out of range
   // per-launch event timing between eii_profile_begin and eii_profile_end
@@ -279,6 +281,8 @@ extern "C" int eii_model_load(const char* path, int device, eii_model** out) {
     L.f_m = L.bits[GATED] == 32 ? std::min(L.f[GATED], L.f[SILU] + L.f[UP]) : L.f[GATED];
     const int shift_s = L.f[QR] + L.f[KR] + 3 - kFScore;
     if (shift_s < 1) { delete M; return fail(EII_E_BOUND, "layer " + std::to_string(l) + ": score shift < 1"); }
+    // the attention kernel evaluates scores in int32 pieces that need shift <= 30 (formats give <= 26)
+    if (shift_s > 30) { delete M; return fail(EII_E_BOUND, "layer " + std::to_string(l) + ": score shift > 30"); }
     if ((rc = check_scalar_shift(21 + L.ln1_f - L.f[NORM1], "norm1")) ||
         (rc = check_scalar_shift(21 + L.ln2_f - L.f[NORM2], "norm2")) ||
         (rc = check_scalar_shift(30 + L.f[QP] - L.f[QR], "q rope")) ||
@@ -399,15 +403,16 @@ extern "C" int eii_model_load(const char* path, int device, eii_model** out) {
 }
 
 static void free_ws(eii_model* m) {
-  void* ps[] = {m->x, m->h, m->qkv, m->ctx, m->gu, m->gated, m->pos};
+  void* ps[] = {m->x, m->h, m->qkv, m->vt, m->ctx, m->gu, m->gated, m->pos};
   for (void* p : ps) if (p) (void)hipFree(p);
-  m->x = nullptr; m->h = nullptr; m->qkv = nullptr; m->ctx = nullptr; m->gu = nullptr; m->gated = nullptr; m->pos = nullptr;
+  m->x = nullptr; m->h = nullptr; m->qkv = nullptr; m->vt = nullptr; m->ctx = nullptr; m->gu = nullptr;
+  m->gated = nullptr; m->pos = nullptr;
   m->ws_rows = 0;
 }
 
 extern "C" void eii_model_free(eii_model* m) {
   if (!m) return;
-  hipSetDevice(m->device);
+  (void)hipSetDevice(m->device);
   free_ws(m);
   if (m->seq_off) (void)hipFree(m->seq_off);
   if (m->rope_owned) { (void)hipFree(m->rope_c); (void)hipFree(m->rope_s); }
@@ -464,6 +469,7 @@ int ensure_ws(eii_model* m, size_t rows) {
   al((void**)&m->x, r * kD * 4);
   al(&m->h, r * kD * 4);
   al((void**)&m->qkv, r * kQKVN * 2);
+  al((void**)&m->vt, vt_bytes((int)r));
   al(&m->ctx, r * kD * 4);
   al((void**)&m->gu, r * 2 * kDFF * 2);
   al(&m->gated, r * kDFF * 4);
@@ -479,8 +485,10 @@ int set_batch(eii_model* m, const std::vector<int32_t>& lens, hipStream_t s) {
   if (lens == m->last_lens) return EII_OK;
   size_t rows = 0;
   std::vector<int32_t> off(lens.size() + 1, 0), pos;
+  int max_kt = 0;
   for (size_t i = 0; i < lens.size(); ++i) {
     off[i + 1] = off[i] + lens[i];
+    max_kt = std::max(max_kt, attn_key_tiles(off[i], lens[i]));
     for (int t = 0; t < lens[i]; ++t) pos.push_back(t);
   }
   rows = pos.size();
@@ -494,6 +502,7 @@ int set_batch(eii_model* m, const std::vector<int32_t>& lens, hipStream_t s) {
   if (rows) HIPCHK(hipMemcpyAsync(m->pos, pos.data(), rows * 4, hipMemcpyHostToDevice, s));
   HIPCHK(hipStreamSynchronize(s));    // the host vectors die at return
   m->last_lens = lens;
+  m->max_kt = max_kt;
   return EII_OK;
 }
 
@@ -525,8 +534,9 @@ int run_block(eii_model* m, int l, int32_t* x, int M, int nseq, int max_T, const
   {
     ProfScope ps(m, EII_K_GEMM_QKV, s);
     GemmArgs g = gemm_args(L.qkv, h, M, m->qkv, 16);
-    if (!tr) {   // q, k, v projections with RoPE applied in the epilogue
+    if (!tr) {   // q, k, v projections with RoPE and the V^T planes in the epilogue
       g.pos = m->pos; g.cosT = m->rope_c; g.sinT = m->rope_s; g.sh_q = sh_q; g.sh_k = sh_k;
+      g.vt = m->vt; g.vt_stride = vt_stride_for(M);
       HIPCHK(gemm(g, hb, EPI_QKV, s));
     } else {
       HIPCHK(gemm(g, hb, EPI_REQ16, s));
@@ -539,12 +549,13 @@ int run_block(eii_model* m, int l, int32_t* x, int M, int nseq, int max_T, const
     HIPCHK(rope(m->qkv, M, m->pos, m->rope_c, m->rope_s, sh_q, L.bits[QR], sh_k, L.bits[KR], s));
     if (tr->q_rope) HIPCHK(copy_cols(tr->q_rope, kD, m->qkv, kQKVN, 0, kD, 2, M, s));
     if (tr->k_rope) HIPCHK(copy_cols(tr->k_rope, 192, m->qkv, kQKVN, kD, 192, 2, M, s));
+    HIPCHK(build_vt(m->qkv, M, m->vt, s));
   }
   const int cb = L.bits[CTX] / 8;
   {
     ProfScope ps(m, EII_K_ATTN, s);
-    AttnArgs a{m->qkv, m->seq_off, m->exp_tab, tr ? tr->attn_ctx : nullptr, (uint8_t*)m->ctx, M, nseq, max_T,
-               L.f[QR] + L.f[KR] + 3 - kFScore, 16 + L.f[VP] - L.f[CTX], L.bits[CTX]};
+    AttnArgs a{m->qkv, m->vt, m->seq_off, m->exp_tab, tr ? tr->attn_ctx : nullptr, (uint8_t*)m->ctx, M, nseq, max_T,
+               m->max_kt, L.f[QR] + L.f[KR] + 3 - kFScore, 16 + L.f[VP] - L.f[CTX], L.bits[CTX]};
     HIPCHK(attention(a, s));
   }
   {
@@ -814,8 +825,26 @@ extern "C" int eii_attention(const int16_t* qkv, const int32_t* seq_off, int nse
   if (bits_c != 16 && bits_c != 32) return fail(EII_E_ARG, "bits_c must be 16 or 32");
   const int shift_s = f_qr + f_kr + 3 - kFScore;
   if (shift_s < 1) return fail(EII_E_BOUND, "score shift < 1");
+  if (shift_s > 30) return fail(EII_E_BOUND, "score shift > 30");
   if (max_T > 16384) return fail(EII_E_BOUND, "sequences longer than 16384 tokens are not supported");
-  AttnArgs a{qkv, seq_off, exp_tab, ctx, nullptr, 0, nseq, max_T, shift_s, 16 + f_v - f_c, bits_c};
-  HIPCHK(attention(a, (hipStream_t)stream));
+  hipStream_t s = (hipStream_t)stream;
+  // the row offsets decide the launch shape: read them back
+  std::vector<int32_t> off(nseq + 1);
+  HIPCHK(hipMemcpyAsync(off.data(), seq_off, off.size() * 4, hipMemcpyDeviceToHost, s));
+  HIPCHK(hipStreamSynchronize(s));
+  int max_kt = 0;
+  for (int i = 0; i < nseq; ++i) {
+    const int T = off[i + 1] - off[i];
+    if (off[i] < 0 || T <= 0 || T > max_T) return fail(EII_E_ARG, "seq_off must increase by 1..max_T per sequence");
+    max_kt = std::max(max_kt, attn_key_tiles(off[i], T));
+  }
+  const int M = off[nseq];
+  uint8_t* vt = nullptr;
+  HIPCHK(hipMallocAsync((void**)&vt, vt_bytes(M), s));
+  AttnArgs a{qkv, vt, seq_off, exp_tab, ctx, nullptr, M, nseq, max_T, max_kt, shift_s, 16 + f_v - f_c, bits_c};
+  hipError_t e = build_vt(qkv, M, vt, s);
+  if (e == hipSuccess) e = attention(a, s);
+  (void)hipFreeAsync(vt, s);
+  if (e != hipSuccess) return fail(EII_E_DEVICE, std::string("eii_attention: ") + hipGetErrorString(e));
   return EII_OK;
 }

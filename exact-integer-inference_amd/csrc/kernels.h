@@ -44,7 +44,18 @@ struct GemmArgs {
   const int32_t* cosT = nullptr;
   const int32_t* sinT = nullptr;
   int sh_q = 0, sh_k = 0;
+  // EPI_QKV: also write v as the key-contiguous V^T limb planes described below, or null
+  uint8_t* vt = nullptr;
+  int vt_stride = 0;
 };
+
+// V^T limb planes for attention: plane 0 = low bytes - 128, plane 1 = signed high bytes of v;
+// each plane [192 rows = 64 kv group + d][vt_stride] bytes, column = token row.  vt_stride is M
+// rounded up to a multiple of 128 (every row a GEMM tile can touch).
+__host__ __device__ inline int vt_stride_for(int M) { return (M + 127) / 128 * 128; }
+inline size_t vt_bytes(int M) { return (size_t)2 * 192 * vt_stride_for(M); }
+// V^T planes from the v columns of qkv [M, 960] (for paths that do not fuse them into the projection)
+hipError_t build_vt(const int16_t* qkv, int M, uint8_t* vt, hipStream_t s);
 
 hipError_t gemm(const GemmArgs& a, int a_bytes, int epi, hipStream_t s);
 hipError_t weight_colsum(const int8_t* W, int N, int K, int32_t* wsum, hipStream_t s);
@@ -73,17 +84,21 @@ hipError_t silu_gate(const int16_t* gu, int M, const int32_t* silu, int sh, int 
                      uint8_t* planes, void* plain, hipStream_t s);
 
 struct AttnArgs {
-  const int16_t* qkv;      // [M, 960]: q rope | k rope | v
+  const int16_t* qkv;      // [M, 960]: q rope | k rope (v is read from vt)
+  const uint8_t* vt;       // V^T limb planes (vt_stride_for(M))
   const int32_t* seq_off;  // [B + 1] row offsets of the sequences
   const int32_t* exp_tab;  // [1537]
   void* ctx;               // plain [M, 576], int16 or int32, or null
   uint8_t* ctx_planes;     // limb planes [bits_c/8][M][576], or null
   int M;
   int B, max_T;
-  int shift_s;             // f_qr + f_kr + 3 - 7
+  int max_kt;              // max over sequences of the 32-row key tiles it spans (attn_key_tiles)
+  int shift_s;             // f_qr + f_kr + 3 - 7, >= 1
   int sh_ctx;              // 16 + f_v - f_c
   int bits_c;
 };
+// 32-row key tiles (aligned to multiples of 32 rows) spanned by a sequence at rows [s0, s0 + T)
+inline int attn_key_tiles(int s0, int T) { return ((s0 + T - 1) >> 5) - (s0 >> 5) + 1; }
 hipError_t attention(const AttnArgs& a, hipStream_t s);
 
 }  // namespace eii

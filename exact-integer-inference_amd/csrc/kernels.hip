@@ -1,12 +1,12 @@
 // gfx950 kernels of the exact integer forward (SmolLM2-135M shape).
 //
-// Integer projections run on v_mfma_i32_16x16x64_i8: activations wider than int8 are split
-// exactly into int8 limb planes while they are staged into LDS (eii_int.h), every limb plane
-// is multiplied with the same int8 weight tile, and the limb partial sums (each below 2^31)
-// are recombined in int64 in the epilogue, which also applies the reference's requantization.
-// The elementwise kernels are one pass over HBM each; attention computes QK and PV as
-// integer MFMA tiles with the reference's three-step exact softmax (row max, exp-table sum,
-// rounded Q0.16 division).
+// Integer projections run on v_mfma_i32_32x32x32_i8: activations wider than int8 travel as
+// exact int8 limb planes (eii_int.h), written by their producers; every limb plane is
+// multiplied with the same int8 weight tile, and the limb partial sums (each below 2^31) are
+// recombined exactly in the epilogue, which also applies the reference's requantization and
+// the fused RoPE, SiLU-gate and residual steps.  The elementwise kernels are one pass over HBM
+// each; attention computes QK and PV as integer MFMA tiles with the reference's three-step
+// exact softmax (row max, exp-table sum, rounded Q0.16 division).
 #include <algorithm>
 #include <type_traits>
 
@@ -23,10 +23,6 @@ namespace {
 constexpr int kBK = 64;          // K block: one MFMA K-step
 constexpr int kLdsRow = 80;      // LDS bytes per 64-byte row: 16-lane b128 reads hit 64 distinct banks
 
-__device__ __forceinline__ v4i mfma(v4i a, v4i b, v4i c) {
-  return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
-}
-
 // Limb planes of 4 int16 values packed in two dwords: (low bytes - 128, high bytes).
 __device__ __forceinline__ uint32_t lo_bytes16(uint32_t d0, uint32_t d1) {
   return ((d0 & 0xFFu) | ((d0 >> 8) & 0xFF00u) | ((d1 << 16) & 0xFF0000u) | ((d1 << 8) & 0xFF000000u)) ^ 0x80808080u;
@@ -34,14 +30,6 @@ __device__ __forceinline__ uint32_t lo_bytes16(uint32_t d0, uint32_t d1) {
 __device__ __forceinline__ uint32_t hi_bytes16(uint32_t d0, uint32_t d1) {
   return ((d0 >> 8) & 0xFFu) | ((d0 >> 16) & 0xFF00u) | ((d1 << 8) & 0xFF0000u) | (d1 & 0xFF000000u);
 }
-// Byte plane i (0 = lowest) of 4 int32 values, biased by -128 unless it is the top byte.
-__device__ __forceinline__ uint32_t byte_plane32(uint4 d, int i) {
-  const int s = 8 * i;
-  uint32_t r = ((d.x >> s) & 0xFFu) | (((d.y >> s) & 0xFFu) << 8) | (((d.z >> s) & 0xFFu) << 16) |
-               (((d.w >> s) & 0xFFu) << 24);
-  return i == 3 ? r : (r ^ 0x80808080u);
-}
-
 // Limb byte l of a W-byte activation v (eii_int.h split_limbs): low bytes biased by -128, the top
 // byte signed.
 __device__ __forceinline__ uint32_t limb_byte(int32_t v, int l, int W) {
@@ -338,25 +326,53 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
           }
       } else {   // EPI_QKV: heads 0..8 q and 9..11 k get RoPE, 12..14 v are stored as they are
         const int head = nblk >> 6;
-        const int shr = head < 9 ? g.sh_q : g.sh_k;
+        if (head >= 12) {
+          // v: int16 rows and, when requested, the V^T limb planes (4 consecutive rows per dword;
+          // rows up to the tile end fit vt_stride, so no row test there)
+          const size_t vcol = (size_t)((head - 12) * 64 + fc) * g.vt_stride, vpl = (size_t)192 * g.vt_stride;
 #pragma unroll
-        for (int tm = 0; tm < C::TM; ++tm)
+          for (int tm = 0; tm < C::TM; ++tm)
 #pragma unroll
-          for (int e = 0; e < 16; ++e) {
-            const int m = row_of(tm, e);
-            if (m >= g.M) continue;
-            const int32_t a1 = value16(tm, 0, e, nc), a2 = value16(tm, 1, e, nc + 32);
-            int32_t o1 = a1, o2 = a2;
-            if (head < 12) {
+            for (int b = 0; b < 4; ++b) {
+              int32_t v1[4], v2[4];
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                const int e = 4 * b + r, m = row_of(tm, e);
+                v1[r] = value16(tm, 0, e, nc);
+                v2[r] = value16(tm, 1, e, nc + 32);
+                if (m < g.M) {
+                  int16_t* op = (int16_t*)g.out + (size_t)m * g.N + nc;
+                  op[0] = (int16_t)v1[r];
+                  op[32] = (int16_t)v2[r];
+                }
+              }
+              if (g.vt) {
+                uint8_t* vp = g.vt + vcol + row_of(tm, 4 * b);
+                const size_t d32 = (size_t)32 * g.vt_stride;
+                *(uint32_t*)vp = limb_word(v1, 0, 2);
+                *(uint32_t*)(vp + vpl) = limb_word(v1, 1, 2);
+                *(uint32_t*)(vp + d32) = limb_word(v2, 0, 2);
+                *(uint32_t*)(vp + d32 + vpl) = limb_word(v2, 1, 2);
+              }
+            }
+        } else {
+          const int shr = head < 9 ? g.sh_q : g.sh_k;
+#pragma unroll
+          for (int tm = 0; tm < C::TM; ++tm)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+              const int m = row_of(tm, e);
+              if (m >= g.M) continue;
+              const int32_t a1 = value16(tm, 0, e, nc), a2 = value16(tm, 1, e, nc + 32);
               const int ps = g.pos[m];
               const double c = (double)g.cosT[ps * 32 + fc], sn = (double)g.sinT[ps * 32 + fc];
-              o1 = rs_sat_f64(fma((double)a1, c, -(double)a2 * sn), shr, -32768.0, 32767.0);
-              o2 = rs_sat_f64(fma((double)a2, c, (double)a1 * sn), shr, -32768.0, 32767.0);
+              const int32_t o1 = rs_sat_f64(fma((double)a1, c, -(double)a2 * sn), shr, -32768.0, 32767.0);
+              const int32_t o2 = rs_sat_f64(fma((double)a2, c, (double)a1 * sn), shr, -32768.0, 32767.0);
+              int16_t* op = (int16_t*)g.out + (size_t)m * g.N + nc;
+              op[0] = (int16_t)o1;
+              op[32] = (int16_t)o2;
             }
-            int16_t* op = (int16_t*)g.out + (size_t)m * g.N + nc;
-            op[0] = (int16_t)o1;
-            op[32] = (int16_t)o2;
-          }
+        }
       }
     }
 #pragma unroll
@@ -553,219 +569,319 @@ __global__ __launch_bounds__(256) void silu_kernel(const int16_t* gu, int M, con
 }
 
 // ------------------------------------------------------------------------------ attention
-// Workgroup = (64-query block, q head, sequence); wave w owns queries q0+16w .. q0+16w+15.
-// Scores are computed transposed, S^T[key][query] = K . Q^T, so a lane holds one query
-// column and the probabilities P[key][query] land directly in the B-operand layout of the
-// PV product ctx^T[d][query] = V^T . P (the K-slot order of an MFMA is free as long as the A
-// and B operands use the same one).  Limb algebra, with x^ = x - 128 split as 256*H + L':
-//   sum_d q k = 65536 sum QH KH + 256 (sum QH KL' + sum QL' KH) + sum QL' KL'
-//               + 128 (sum_d q^ + sum_d k^) + 64 * 128^2
-//   sum_j P v = 2^24 sum P2 VH + 2^16 (sum P1' VH + sum P2 VL') + 2^8 (sum P0' VH + sum P1' VL')
-//               + sum P0' VL' + 32896 sum_j v^ + 128 sum_j P
-// with P = 65536 P2 + 256 (P1' + 128) + (P0' + 128).
-template <int OB>
-__global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
-  __shared__ __attribute__((aligned(16))) uint8_t kpl[2][64 * kLdsRow];   // K planes, row = key
-  __shared__ __attribute__((aligned(16))) uint8_t vpl[2][64 * kLdsRow];   // V^T planes, row = d
-  __shared__ int32_t sk[64];
-  __shared__ int64_t cv[64];
-  __shared__ int32_t etab[kDMax + 1];
+// Workgroup = the 3 query heads of one kv group for 32 queries of one sequence (wave w = head
+// 3 kvg + w); the workgroups of the longest query tiles are dispatched first.
+//
+// Scores run on v_mfma_i32_32x32x32_i8 as S^T[key][query] = K . Q^T over the head dimension (two
+// K-steps of 32) with q = 256 QH + (QL' + 128), QL' = low byte - 128, QH = signed high byte, and
+// k likewise.  A-operand row i carries key pi(i) = 16 ((i >> 2) & 1) + 4 (i >> 3) + (i & 3) of the
+// key tile, the key that output row i denotes, so lane 32 h + c ends with query c and keys
+// 16 h + j (output register j) of the tile: 16 consecutive keys of one query, which is the
+// B-operand layout of ctx^T[d][query] = sum_key V^T[d][key] P^T[key][query] with operand byte j =
+// key 16 h + j.  V^T limb planes (kernels.h) supply the matching A operand.  Key tiles are 32-row
+// blocks aligned to row 0 of the batch; keys outside [sequence start, query] are masked.
+//
+// Exact sums (all partial MFMA sums fit int32):
+//   sum_d q k = 65536 S_HH + 256 (S_HL + S_LH) + S_LL + 128 (sum_d q + sum_d k) - 2^20
+//   sum_key P v = 65536 C_1H + 256 (C_1L + C_0H) + C_0L + 128 sum_key P
+// where P = 256 R1 + P0 with P0 = sext(P & 255) and R1 = (P + 128) >> 8 in [0, 256] (R1 goes
+// into the MFMA as up to three int8 parts): a key with P = 0 adds nothing, so masked keys and
+// the rows beyond a sequence need no correction terms.
+//
+// NKT > 0: the packed int16 scores of up to NKT key tiles stay in registers between the row-max,
+// exp-sum and probability passes; NKT == 0: every pass recomputes the scores (long sequences).
+constexpr int32_t kMasked = -32768;   // no score exceeds it, so the row max never picks it
 
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, gq = lane >> 4, c16 = lane & 15;
-  const int b = blockIdx.z, hh = blockIdx.y, qb = gridDim.x - 1 - blockIdx.x;
-  const int s0 = a.seq_off[b], T = a.seq_off[b + 1] - s0, q0 = qb * 64;
-  if (q0 >= T) return;
-  const int kvg = hh / 3;
-  const int qi = q0 + 16 * w + c16;
-
-  for (int i = tid; i <= kDMax; i += 256) etab[i] = a.exp_tab[i];
-  if (tid < 64) cv[tid] = 0;
-
-  // Q B-fragment: query qi, d = 16*gq .. 16*gq+15
-  v4i QH, QL;
-  int32_t sq;
-  {
-    uint4 d0 = make_uint4(0, 0, 0, 0), d1 = d0;
-    if (qi < T) {
-      const int16_t* qp = a.qkv + (size_t)(s0 + qi) * kQKVN + hh * 64 + 16 * gq;
-      d0 = *(const uint4*)qp;
-      d1 = *(const uint4*)(qp + 8);
-    }
-    QL = v4i{(int)lo_bytes16(d0.x, d0.y), (int)lo_bytes16(d0.z, d0.w), (int)lo_bytes16(d1.x, d1.y),
-             (int)lo_bytes16(d1.z, d1.w)};
-    QH = v4i{(int)hi_bytes16(d0.x, d0.y), (int)hi_bytes16(d0.z, d0.w), (int)hi_bytes16(d1.x, d1.y),
-             (int)hi_bytes16(d1.z, d1.w)};
-    const uint32_t dw[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
-    sq = 0;
+__device__ __forceinline__ int32_t sum16x8(u32x4 d) {   // sum of the 8 int16 values in d
+  int32_t s = 0;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) sq += (int32_t)(int16_t)(dw[i] & 0xFFFF) + (int32_t)(int16_t)(dw[i] >> 16);
-    sq += __shfl_xor(sq, 16);
-    sq += __shfl_xor(sq, 32);
-    sq -= 64 * 128;
+  for (int i = 0; i < 4; ++i) s += ((int32_t)(d[i] << 16) >> 16) + ((int32_t)d[i] >> 16);
+  return s;
+}
+
+template <int OB, int NKT>
+__global__ __launch_bounds__(192) void attn_kernel(AttnArgs a) {
+  __shared__ int32_t etab[kDMax + 2];                        // exp table, etab[1537] = 0
+  __shared__ __attribute__((aligned(16))) int32_t skl[3][32];   // per wave: 128 * sum_d k per key
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, c = lane & 31, h = lane >> 5;
+  const int seq = blockIdx.x, kvg = blockIdx.y, qt = gridDim.z - 1 - blockIdx.z;
+  const int s0 = a.seq_off[seq], T = a.seq_off[seq + 1] - s0;
+  if (32 * qt >= T) return;
+  for (int i = tid; i < kDMax + 2; i += 192) etab[i] = i <= kDMax ? a.exp_tab[i] : 0;
+  __syncthreads();
+
+  const int hh = 3 * kvg + w;
+  const int q0 = s0 + 32 * qt, qlast = min(q0 + 31, s0 + T - 1), qi = q0 + c;
+  const int g0 = s0 >> 5, ntile = (qlast >> 5) - g0 + 1;
+  const int pic = 16 * ((c >> 2) & 1) + 4 * (c >> 3) + (c & 3);
+  const int sh = a.shift_s;
+  const int vts = vt_stride_for(a.M);
+
+  // B operand: query qi (rows past the sequence read its last row), d = 32 s + 16 h + 0..15
+  v4i ql[2], qh[2];
+  int32_t cq;
+  {
+    const int16_t* qp = a.qkv + (size_t)min(qi, qlast) * kQKVN + hh * 64 + 16 * h;
+    int32_t sum = 0;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const u32x4 d0 = *(const u32x4*)(qp + 32 * s), d1 = *(const u32x4*)(qp + 32 * s + 8);
+      ql[s] = v4i{(int)lo_bytes16(d0[0], d0[1]), (int)lo_bytes16(d0[2], d0[3]), (int)lo_bytes16(d1[0], d1[1]),
+                  (int)lo_bytes16(d1[2], d1[3])};
+      qh[s] = v4i{(int)hi_bytes16(d0[0], d0[1]), (int)hi_bytes16(d0[2], d0[3]), (int)hi_bytes16(d1[0], d1[1]),
+                  (int)hi_bytes16(d1[2], d1[3])};
+      sum += sum16x8(d0) + sum16x8(d1);
+    }
+    sum += __shfl_xor(sum, 32);
+    cq = 128 * sum - (1 << 20) + (1 << (sh - 1));   // with the rounding offset of RS(., sh)
   }
 
-  const int nkb = min(qb + 1, (T + 63) / 64);
-  int32_t rowmax = -(1 << 20);
-  int64_t Z = 0, SP = 0;
-  double rZ = 0.0;
-  v4i C24[4], C16[4], C8[4], C0[4];
+  // Scores SAT16(RS(q.k, sh)) of key tile g for this lane's query, keys 16 h + j.  The sum
+  // acc + 2^(sh-1) = 65536 wv + lo16 with lo16 in [0, 65536) is evaluated in int32 pieces.
+  auto scores = [&](int g, int32_t (&sc)[16]) __attribute__((always_inline)) {
+    const int16_t* kp = a.qkv + (size_t)min(32 * g + pic, a.M - 1) * kQKVN + kD + kvg * 64 + 16 * h;
+    v4i kl[2], kh[2];
+    int32_t ks = 0;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) C24[i] = C16[i] = C8[i] = C0[i] = v4i{0, 0, 0, 0};
-
-  for (int pass = 0; pass < 3; ++pass) {
-    for (int kb = 0; kb < nkb; ++kb) {
-      __syncthreads();
-      // stage K (and in the last pass V^T) for keys kb*64 .. kb*64+63
+    for (int s = 0; s < 2; ++s) {
+      const u32x4 d0 = *(const u32x4*)(kp + 32 * s), d1 = *(const u32x4*)(kp + 32 * s + 8);
+      kl[s] = v4i{(int)lo_bytes16(d0[0], d0[1]), (int)lo_bytes16(d0[2], d0[3]), (int)lo_bytes16(d1[0], d1[1]),
+                  (int)lo_bytes16(d1[2], d1[3])};
+      kh[s] = v4i{(int)hi_bytes16(d0[0], d0[1]), (int)hi_bytes16(d0[2], d0[3]), (int)hi_bytes16(d1[0], d1[1]),
+                  (int)hi_bytes16(d1[2], d1[3])};
+      ks += sum16x8(d0) + sum16x8(d1);
+    }
+    ks += __shfl_xor(ks, 32);
+    skl[w][pic] = 128 * ks;   // lanes c and c + 32 store the same value
+    __builtin_amdgcn_wave_barrier();
+    v16i a16 = v16i{}, a8 = v16i{}, a0 = v16i{};
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int q = tid + 256 * i, jj = q >> 3, c = q & 7, j = kb * 64 + jj;
-        uint4 d = make_uint4(0, 0, 0, 0);
-        if (j < T) d = *(const uint4*)(a.qkv + (size_t)(s0 + j) * kQKVN + kD + kvg * 64 + 8 * c);
-        *(uint2*)(&kpl[0][jj * kLdsRow + 8 * c]) = make_uint2(lo_bytes16(d.x, d.y), lo_bytes16(d.z, d.w));
-        *(uint2*)(&kpl[1][jj * kLdsRow + 8 * c]) = make_uint2(hi_bytes16(d.x, d.y), hi_bytes16(d.z, d.w));
-        int32_t s = 0;
-        const uint32_t dw[4] = {d.x, d.y, d.z, d.w};
+    for (int s = 0; s < 2; ++s) {
+      a16 = mfma32(kh[s], qh[s], a16);
+      a8 = mfma32(kh[s], ql[s], a8);
+      a8 = mfma32(kl[s], qh[s], a8);
+      a0 = mfma32(kl[s], ql[s], a0);
+    }
+    const v4i* kk = (const v4i*)&skl[w][16 * h];
+    const v4i k4[4] = {kk[0], kk[1], kk[2], kk[3]};
+    __builtin_amdgcn_wave_barrier();
+    const bool edge = 32 * g < s0 || 32 * g + 31 > q0;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) s += (int32_t)(int16_t)(dw[e] & 0xFFFF) + (int32_t)(int16_t)(dw[e] >> 16);
-        s += __shfl_xor(s, 1);
-        s += __shfl_xor(s, 2);
-        s += __shfl_xor(s, 4);
-        if (c == 0) sk[jj] = s - 64 * 128;
-        if (pass == 2) {
-          uint4 dv = make_uint4(0, 0, 0, 0);
-          if (j < T) dv = *(const uint4*)(a.qkv + (size_t)(s0 + j) * kQKVN + kD + 192 + kvg * 64 + 8 * c);
-          const uint32_t vw[4] = {dv.x, dv.y, dv.z, dv.w};
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const uint32_t v16 = (vw[e >> 1] >> (16 * (e & 1))) & 0xFFFF;
-            const int dd = 8 * c + e;
-            vpl[0][dd * kLdsRow + jj] = (uint8_t)((v16 & 0xFF) ^ 0x80);
-            vpl[1][dd * kLdsRow + jj] = (uint8_t)(v16 >> 8);
-          }
-        }
+    for (int j = 0; j < 16; ++j) {
+      const int32_t lo = a8[j] * 256 + a0[j] + k4[j >> 2][j & 3] + cq;
+      const int32_t wv = a16[j] + (lo >> 16);
+      int32_t v = sh >= 16 ? wv >> (sh - 16)
+                           : min(max(wv, -32769), 32768) * (1 << (16 - sh)) + ((lo & 0xFFFF) >> sh);
+      v = min(max(v, -32768), 32767);
+      if (edge) {
+        const int key = 32 * g + 16 * h + j;
+        if (key < s0 || key > qi) v = kMasked;
       }
-      __syncthreads();
-      if (pass == 2 && tid < 64) {
-        int32_t s = 0;
-        for (int jj = 0; jj < 64; ++jj)
-          s += (int32_t)(int8_t)vpl[1][tid * kLdsRow + jj] * 256 + (int32_t)(int8_t)vpl[0][tid * kLdsRow + jj];
-        cv[tid] += s;
-      }
+      sc[j] = v;
+    }
+  };
+  // e = E[rowmax - s] for d <= 1536, else 0; masked keys 0
+  auto expo = [&](int g, int j, int32_t s, int32_t rowmax) __attribute__((always_inline)) -> int32_t {
+    const int32_t e = etab[min(rowmax - s, kDMax + 1)];
+    if (32 * g < s0 || 32 * g + 31 > q0) {
+      const int key = 32 * g + 16 * h + j;
+      if (key < s0 || key > qi) return 0;
+    }
+    return e;
+  };
 
-      // scores for keys kb*64 + kt*16 + 4*gq + r, query qi
-      int32_t sc[4][4];
+  v16i C16[2], C8[2], C0[2];
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
-        const v4i KH = *(const v4i*)(&kpl[1][(kt * 16 + c16) * kLdsRow + 16 * gq]);
-        const v4i KL = *(const v4i*)(&kpl[0][(kt * 16 + c16) * kLdsRow + 16 * gq]);
-        const v4i z = v4i{0, 0, 0, 0};
-        const v4i a16 = mfma(KH, QH, z);
-        v4i a8 = mfma(KH, QL, z);
-        a8 = mfma(KL, QH, a8);
-        const v4i a0 = mfma(KL, QL, z);
+  for (int i = 0; i < 2; ++i) C16[i] = C8[i] = C0[i] = v16i{};
+  int32_t SP = 0;
+  double Zd = 0.0, rZ = 0.0, Zh = 0.0;
+  // P = floor((e 65536 + floor(Z / 2)) / Z) (python/intref.py:245-246): the float64 quotient is
+  // within one of the truth and the exact float64 remainder corrects it
+  auto prob = [&](int32_t e) __attribute__((always_inline)) -> int32_t {
+    const double num = fma((double)e, 65536.0, Zh);
+    const double q = floor(num * rZ);
+    const double rem = fma(-q, Zd, num);
+    return (int32_t)q + (rem >= Zd ? 1 : 0) - (rem < 0.0 ? 1 : 0);
+  };
+  // probabilities of key tile g (e values) into limb operands, then the P.V MFMAs.  R1 =
+  // (P + 128) >> 8 in [0, 256] goes in as P1 = min(R1, 127) plus, in the waves where some R1
+  // exceeds 127 (a key holding about half the weight or more), P1b = min(R1 - P1, 127) and
+  // P1c = R1 - P1 - P1b, all with the weight of P1.
+  auto pv = [&](int g, const int32_t (&ev)[16]) __attribute__((always_inline)) {
+    uint32_t w0[4], w1[4];
+    int32_t rest[16];
+    int32_t anyrest = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t b0 = 0, b1 = 0;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int32_t P = prob(ev[4 * i + r]);
+        SP += P;
+        const int32_t R1 = (P + 128) >> 8, p1 = min(R1, 127);
+        rest[4 * i + r] = R1 - p1;
+        anyrest |= R1 - p1;
+        b0 |= ((uint32_t)P & 0xFFu) << (8 * r);
+        b1 |= (uint32_t)p1 << (8 * r);
+      }
+      w0[i] = b0; w1[i] = b1;
+    }
+    const v4i P0 = v4i{(int)w0[0], (int)w0[1], (int)w0[2], (int)w0[3]};
+    const v4i P1 = v4i{(int)w1[0], (int)w1[1], (int)w1[2], (int)w1[3]};
+    const size_t vpl = (size_t)192 * vts;
+    v4i VL[2], VH[2];
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt) {
+      const uint8_t* vp = a.vt + (size_t)(kvg * 64 + 32 * dt + c) * vts + 32 * g + 16 * h;
+      VL[dt] = *(const v4i*)vp;
+      VH[dt] = *(const v4i*)(vp + vpl);
+    }
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt) {
+      C16[dt] = mfma32(VH[dt], P1, C16[dt]);
+      C8[dt] = mfma32(VH[dt], P0, C8[dt]);
+      C8[dt] = mfma32(VL[dt], P1, C8[dt]);
+      C0[dt] = mfma32(VL[dt], P0, C0[dt]);
+    }
+    if (__any(anyrest != 0)) {
+      uint32_t wb[4], wc[4];
+      int32_t anyc = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        uint32_t bb = 0, bc = 0;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int jj = kt * 16 + 4 * gq + r;
-          const int64_t acc = (int64_t)a16[r] * 65536 + (int64_t)a8[r] * 256 + a0[r] +
-                              128 * (int64_t)(sk[jj] + sq) + (1 << 20);
-          sc[kt][r] = (int32_t)clamp_bits16(rs(acc, a.shift_s));
+          const int32_t rb = min(rest[4 * i + r], 127), rc = rest[4 * i + r] - rb;
+          anyc |= rc;
+          bb |= (uint32_t)rb << (8 * r);
+          bc |= (uint32_t)rc << (8 * r);
+        }
+        wb[i] = bb; wc[i] = bc;
+      }
+      const v4i P1b = v4i{(int)wb[0], (int)wb[1], (int)wb[2], (int)wb[3]};
+      const v4i P1c = v4i{(int)wc[0], (int)wc[1], (int)wc[2], (int)wc[3]};
+      const bool three = __any(anyc != 0);
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt) {
+        C16[dt] = mfma32(VH[dt], P1b, C16[dt]);
+        C8[dt] = mfma32(VL[dt], P1b, C8[dt]);
+        if (three) {
+          C16[dt] = mfma32(VH[dt], P1c, C16[dt]);
+          C8[dt] = mfma32(VL[dt], P1c, C8[dt]);
         }
       }
+    }
+  };
+  auto set_z = [&](int64_t Z) __attribute__((always_inline)) {
+    Z += __shfl_xor(Z, 32);
+    Zd = (double)Z;
+    rZ = 1.0 / Zd;
+    Zh = (double)(Z >> 1);
+  };
 
-      if (pass == 0) {
+  int32_t rowmax = kMasked;
+  if constexpr (NKT > 0) {
+    uint32_t pk[NKT][8];   // packed int16 scores
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
+    for (int t = 0; t < NKT; ++t) {
+      if (t < ntile) {
+        int32_t sc[16];
+        scores(g0 + t, sc);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int j = kb * 64 + kt * 16 + 4 * gq + r;
-            if (j <= qi && sc[kt][r] > rowmax) rowmax = sc[kt][r];
-          }
-      } else {
-        uint32_t p2w[4], p1w[4], p0w[4];
-        bool any2 = false;
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt) {
-          p2w[kt] = p1w[kt] = p0w[kt] = 0;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int j = kb * 64 + kt * 16 + 4 * gq + r;
-            const int dd = rowmax - sc[kt][r];
-            const int64_t e = (j <= qi && dd <= kDMax) ? etab[dd] : 0;
-            if (pass == 1) {
-              Z += e;
-            } else {
-              const int64_t P = attn_prob(e, Z, rZ);
-              SP += P;
-              const uint32_t p = (uint32_t)P;
-              p2w[kt] |= (p >> 16) << (8 * r);
-              p1w[kt] |= (((p >> 8) & 0xFFu) ^ 0x80u) << (8 * r);
-              p0w[kt] |= ((p & 0xFFu) ^ 0x80u) << (8 * r);
-              any2 |= (p >> 16) != 0;
-            }
-          }
-        }
-        if (pass == 2) {
-          const v4i P2 = v4i{(int)p2w[0], (int)p2w[1], (int)p2w[2], (int)p2w[3]};
-          const v4i P1 = v4i{(int)p1w[0], (int)p1w[1], (int)p1w[2], (int)p1w[3]};
-          const v4i P0 = v4i{(int)p0w[0], (int)p0w[1], (int)p0w[2], (int)p0w[3]};
-          const bool wave2 = __any(any2);
-#pragma unroll
-          for (int dt = 0; dt < 4; ++dt) {
-            const int dd = dt * 16 + c16;
-            v4i VH, VL;
-#pragma unroll
-            for (int kt = 0; kt < 4; ++kt) {
-              VH[kt] = *(const int*)(&vpl[1][dd * kLdsRow + 16 * kt + 4 * gq]);
-              VL[kt] = *(const int*)(&vpl[0][dd * kLdsRow + 16 * kt + 4 * gq]);
-            }
-            C16[dt] = mfma(VH, P1, C16[dt]);
-            C8[dt] = mfma(VH, P0, C8[dt]);
-            C8[dt] = mfma(VL, P1, C8[dt]);
-            C0[dt] = mfma(VL, P0, C0[dt]);
-            if (wave2) {
-              C24[dt] = mfma(VH, P2, C24[dt]);
-              C16[dt] = mfma(VL, P2, C16[dt]);
-            }
-          }
+        for (int i = 0; i < 8; ++i) {
+          pk[t][i] = ((uint32_t)sc[2 * i] & 0xFFFFu) | ((uint32_t)sc[2 * i + 1] << 16);
+          rowmax = max(rowmax, max(sc[2 * i], sc[2 * i + 1]));
         }
       }
     }
-    if (pass == 0) {
-      rowmax = max(rowmax, __shfl_xor(rowmax, 16));
-      rowmax = max(rowmax, __shfl_xor(rowmax, 32));
-    } else if (pass == 1) {
-      Z += __shfl_xor(Z, 16);
-      Z += __shfl_xor(Z, 32);
-      rZ = 1.0 / (double)Z;
-    } else {
-      SP += __shfl_xor(SP, 16);
-      SP += __shfl_xor(SP, 32);
+    rowmax = max(rowmax, __shfl_xor(rowmax, 32));
+    auto unpack = [&](int t, int j) __attribute__((always_inline)) -> int32_t {
+      const uint32_t p = pk[t][j >> 1];
+      return (j & 1) ? (int32_t)p >> 16 : (int32_t)(p << 16) >> 16;
+    };
+    int64_t Z = 0;
+#pragma unroll
+    for (int t = 0; t < NKT; ++t)
+      if (t < ntile) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) Z += expo(g0 + t, j, unpack(t, j), rowmax);
+      }
+    set_z(Z);
+#pragma unroll
+    for (int t = 0; t < NKT; ++t)
+      if (t < ntile) {
+        int32_t ev[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) ev[j] = expo(g0 + t, j, unpack(t, j), rowmax);
+        pv(g0 + t, ev);
+      }
+  } else {
+#pragma unroll 1
+    for (int t = 0; t < ntile; ++t) {
+      int32_t sc[16];
+      scores(g0 + t, sc);
+#pragma unroll
+      for (int j = 0; j < 16; ++j) rowmax = max(rowmax, sc[j]);
+    }
+    rowmax = max(rowmax, __shfl_xor(rowmax, 32));
+    int64_t Z = 0;
+#pragma unroll 1
+    for (int t = 0; t < ntile; ++t) {
+      int32_t sc[16];
+      scores(g0 + t, sc);
+#pragma unroll
+      for (int j = 0; j < 16; ++j) Z += expo(g0 + t, j, sc[j], rowmax);
+    }
+    set_z(Z);
+#pragma unroll 1
+    for (int t = 0; t < ntile; ++t) {
+      int32_t sc[16];
+      scores(g0 + t, sc);
+#pragma unroll
+      for (int j = 0; j < 16; ++j) sc[j] = expo(g0 + t, j, sc[j], rowmax);
+      pv(g0 + t, sc);
     }
   }
-  __syncthreads();
-  if (qi >= T) return;
-  const size_t orow = (size_t)(s0 + qi) * kD + hh * 64;
+  SP += __shfl_xor(SP, 32);
+
+  if (qi > qlast) return;
+  // ctx of query qi, d = 32 dt + 8 b + 4 h + r (output register 4 b + r of tile dt)
+  const size_t orow = (size_t)qi * kD + hh * 64, pl = (size_t)a.M * kD;
 #pragma unroll
-  for (int dt = 0; dt < 4; ++dt) {
-    int32_t cvals[4];
+  for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int d = dt * 16 + 4 * gq + r;
-      const int64_t acc = (int64_t)C24[dt][r] * (1LL << 24) + (int64_t)C16[dt][r] * 65536 +
-                          (int64_t)C8[dt][r] * 256 + C0[dt][r] + 32896 * cv[d] + 128 * SP;
-      cvals[r] = (int32_t)sat(rs(acc, a.sh_ctx), a.bits_c);
-    }
-    const int d0 = dt * 16 + 4 * gq;
-    if (a.ctx_planes) {
-      const size_t pl = (size_t)a.M * kD;
+    for (int b = 0; b < 4; ++b) {
+      int32_t cv[4];
 #pragma unroll
-      for (int l = 0; l < OB; ++l) *(uint32_t*)(a.ctx_planes + l * pl + orow + d0) = limb_word(cvals, l, OB);
+      for (int r = 0; r < 4; ++r) {
+        const int j = 4 * b + r;
+        const int64_t acc = (int64_t)C16[dt][j] * 65536 + (int64_t)C8[dt][j] * 256 + C0[dt][j] + 128 * (int64_t)SP;
+        cv[r] = (int32_t)sat(rs(acc, a.sh_ctx), a.bits_c);
+      }
+      const int d0 = 32 * dt + 8 * b + 4 * h;
+      if (a.ctx_planes) {
+#pragma unroll
+        for (int l = 0; l < OB; ++l) *(uint32_t*)(a.ctx_planes + l * pl + orow + d0) = limb_word(cv, l, OB);
+      }
+      if (a.ctx) {
+        if constexpr (OB == 2) *(uint2*)((int16_t*)a.ctx + orow + d0) = make_uint2(pack16(cv[0], cv[1]), pack16(cv[2], cv[3]));
+        else *(int4*)((int32_t*)a.ctx + orow + d0) = make_int4(cv[0], cv[1], cv[2], cv[3]);
+      }
     }
-    if (a.ctx) {
-      if constexpr (OB == 2) *(uint2*)((int16_t*)a.ctx + orow + d0) = make_uint2(pack16(cvals[0], cvals[1]), pack16(cvals[2], cvals[3]));
-      else *(int4*)((int32_t*)a.ctx + orow + d0) = make_int4(cvals[0], cvals[1], cvals[2], cvals[3]);
-    }
-  }
+}
+
+// V^T limb planes from qkv: thread = (d row, 4 consecutive token rows)
+__global__ __launch_bounds__(256) void vt_kernel(const int16_t* qkv, int M, uint8_t* vt, int stride) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x, ng = (size_t)stride / 4;
+  if (i >= 192 * ng) return;
+  const int d = (int)(i / ng), m0 = (int)(4 * (i % ng));
+  int32_t v[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) v[r] = qkv[(size_t)min(m0 + r, M - 1) * kQKVN + kD + 192 + d];
+  uint8_t* p = vt + (size_t)d * stride + m0;
+  *(uint32_t*)p = limb_word(v, 0, 2);
+  *(uint32_t*)(p + (size_t)192 * stride) = limb_word(v, 1, 2);
 }
 
 inline unsigned blocks_for(size_t n) { return (unsigned)((n + 255) / 256); }
@@ -841,9 +957,22 @@ hipError_t silu_gate(const int16_t* gu, int M, const int32_t* silu, int sh, int 
 
 hipError_t attention(const AttnArgs& a, hipStream_t s) {
   if (a.B <= 0 || a.max_T <= 0) return hipSuccess;
-  dim3 grid((a.max_T + 63) / 64, kNH, a.B);
-  if (a.bits_c == 16) hipLaunchKernelGGL(attn_kernel<2>, grid, dim3(256), 0, s, a);
-  else hipLaunchKernelGGL(attn_kernel<4>, grid, dim3(256), 0, s, a);
+  if (!a.vt || a.shift_s < 1 || a.shift_s > 30 || a.max_kt < 1) return hipErrorInvalidValue;
+  const dim3 grid(a.B, kNKV, (a.max_T + 31) / 32), block(192);
+  // up to 8 key tiles (256 keys) the scores stay in registers; beyond, every pass recomputes them
+  if (a.max_kt <= 8) {
+    if (a.bits_c == 16) hipLaunchKernelGGL((attn_kernel<2, 8>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((attn_kernel<4, 8>), grid, block, 0, s, a);
+  } else {
+    if (a.bits_c == 16) hipLaunchKernelGGL((attn_kernel<2, 0>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((attn_kernel<4, 0>), grid, block, 0, s, a);
+  }
+  return hipGetLastError();
+}
+
+hipError_t build_vt(const int16_t* qkv, int M, uint8_t* vt, hipStream_t s) {
+  const int stride = vt_stride_for(M);
+  hipLaunchKernelGGL(vt_kernel, dim3(blocks_for((size_t)192 * (stride / 4))), dim3(256), 0, s, qkv, M, vt, stride);
   return hipGetLastError();
 }
 

@@ -36,6 +36,17 @@ FILE_BYTES = HEADER_BYTES + NL * LAYER_BYTES
 assert FILE_BYTES == 154045048
 
 
+def matrix_offset(layer, name):
+    """Byte offset of matrix `name`'s int8 rows in layer `layer` (then m i64[N], n i64[N])."""
+    off = HEADER_BYTES + layer * LAYER_BYTES + 24 * 8 + 2 * (D * 8 + 8)
+    for m in MATS:
+        if m == name:
+            return off
+        n, k = MAT_NK[m]
+        off += n * k + 2 * n * 8
+    raise KeyError(name)
+
+
 class ModelBin:
     """Typed views over a model.bin image (a numpy memmap or an in-memory buffer).
 

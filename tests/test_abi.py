@@ -1,0 +1,71 @@
+"""The C ABI without a GPU: libeii.so loads, exports every entry point include/eii.h declares
+(with the ctypes signatures eii/lib.py binds), and rejects bad arguments and malformed model
+files with the documented status codes before touching a device."""
+import ctypes as C
+import os
+import re
+import shutil
+
+import numpy as np
+import pytest
+
+from eii import lib as L
+from eii import modelbin
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "eii.h")
+
+
+def declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(eii_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_and_binding_agree():
+    names = declared()
+    assert len(names) >= 20
+    assert set(names) == set(L.SIGNATURES), set(names) ^ set(L.SIGNATURES)
+
+
+def test_library_exports_every_entry_point():
+    lib = L.load()
+    for n in declared():
+        assert hasattr(lib, n), n
+
+
+def test_argument_errors_need_no_device():
+    lib = L.load()
+    assert lib.eii_gemm_i8(None, 16, None, 4, 4, 64, None, None) == L.EII_E_ARG
+    a = (C.c_int16 * 64)()
+    w = (C.c_int8 * 256)()
+    assert lib.eii_gemm_i8(a, 8, w, 1, 4, 64, None, None) == L.EII_E_ARG        # a_bits
+    assert lib.eii_gemm_i8(a, 16, w, 1, 4, 100, None, None) == L.EII_E_ARG      # K
+    assert b"K must be" in lib.eii_last_error()
+    assert lib.eii_linear(a, 16, w, None, None, None, 1, 4, 64, 16, None, None) == L.EII_E_ARG
+    assert lib.eii_rmsnorm(None, 1, None, 14, 11, 16, None, None) == L.EII_E_ARG
+    assert lib.eii_attention(None, None, 1, 4, None, 10, 10, 11, 11, 16, None, None) == L.EII_E_ARG
+    h = C.c_void_p()
+    assert lib.eii_model_load(None, 0, C.byref(h)) == L.EII_E_ARG
+    assert lib.eii_forward(None, None, 1, 1, None, None, None, None) == L.EII_E_ARG
+    assert lib.eii_model_rope_rows(None) == 0
+
+
+def test_model_file_errors(tmp_path, model_path):
+    lib = L.load()
+    h = C.c_void_p()
+    missing = str(tmp_path / "none.bin").encode()
+    assert lib.eii_model_load(missing, 0, C.byref(h)) == L.EII_E_IO
+    short = tmp_path / "short.bin"
+    short.write_bytes(b"\0" * 1000)
+    assert lib.eii_model_load(str(short).encode(), 0, C.byref(h)) == L.EII_E_IO
+    assert b"bytes" in lib.eii_last_error()
+    # a requantization shift n + f_in - f_out below 1 (python/intref.py:49 asserts >= 1)
+    bad = tmp_path / "bad.bin"
+    shutil.copyfile(model_path, bad)
+    off = modelbin.matrix_offset(0, "q") + 576 * 576 + 8 * 576    # n[0] of layer 0's q_proj
+    with open(bad, "r+b") as f:
+        f.seek(off)
+        f.write(np.array([-40], dtype="<i8").tobytes())
+    assert lib.eii_model_load(str(bad).encode(), 0, C.byref(h)) == L.EII_E_BOUND
+    assert not h.value

@@ -29,6 +29,8 @@ PEAK_HBM = 8.0e12               # bytes/s
 V, D, DFF, NL = 49152, 576, 1536, 30
 REF_BIN = os.path.join(ROOT, "oracle", "_ref", "intref")
 GOLDEN = os.path.join(ROOT, "tests", "golden", "golden.json")
+PROFILES = os.path.join(ROOT, "profiles")
+COPY_BYTES = 1 << 30            # --copy-calibration: one plain device copy of 1 GiB
 
 
 def sha(a):
@@ -78,6 +80,36 @@ def cpu_baseline_reference(model_path, ids, out):
             "seconds": cpu_s, "wall_seconds": wall, "verdict": last, "states_checked_by_reference": r.returncode == 0}
 
 
+def measured_traffic(kernel, config):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 counter summary
+    profiles/<kernel>_<config>_traffic.txt (FETCH_SIZE + WRITE_SIZE, scaled by the same counters
+    on a plain copy of known size), or None when no summary exists for it."""
+    path = os.path.join(PROFILES, f"{kernel}_{config}_traffic.txt")
+    if not os.path.exists(path):
+        return None
+    vals = {}
+    for line in open(path):
+        if ":" in line and line.split(":")[0].strip() in ("fetch_bytes_per_launch", "write_bytes_per_launch"):
+            vals[line.split(":")[0].strip()] = float(line.split(":")[1])
+    if len(vals) != 2:
+        return None
+    return {"bytes": vals["fetch_bytes_per_launch"] + vals["write_bytes_per_launch"],
+            "fetch": vals["fetch_bytes_per_launch"], "write": vals["write_bytes_per_launch"],
+            "source": os.path.relpath(path, ROOT)}
+
+
+def copy_calibration():
+    """A plain device copy of COPY_BYTES, for scaling the HBM byte counters (run under rocprofv3)."""
+    import torch
+    src = torch.ones(COPY_BYTES, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": COPY_BYTES, "launches": 3}))
+
+
 def cpu_baseline_port(model_path, ids):
     sys.path.insert(0, ROOT)
     from oracle.intref_np import OracleModel
@@ -97,7 +129,12 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="cfg4")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a 1 GiB device copy (the byte-counter calibration) and exit")
     args = ap.parse_args()
+    if args.copy_calibration:
+        copy_calibration()
+        return
     if args.gpus != 1:
         print(f"bench.py: this engine runs on one GPU (sequences shard across GPUs with no exchange, "
               f"which this build does not launch); --gpus {args.gpus} is not supported", file=sys.stderr)
@@ -179,6 +216,7 @@ def main():
         else:
             cpu = cpu_baseline_port(model_path, ids_np)
 
+    traffic = measured_traffic(dom, args.config)
     res = {
         "metric": "bit-exact tokens/s, 135M int fwd at B=256; int GEMM % of int8 MFMA peak",
         "value": value, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -191,7 +229,9 @@ def main():
                    "parallelism": "single GPU"},
         "exact_sampled_sequences": exact,
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": achieved / 1e12, "peak": PEAK_INT8_OPS / 1e12,
-                     "unit": "TFLOP/s", "frac": achieved / PEAK_INT8_OPS, "traffic": None,
+                     "unit": "TFLOP/s", "frac": achieved / PEAK_INT8_OPS,
+                     "traffic": traffic["bytes"] if traffic else None,
+                     "traffic_detail": traffic,
                      "ops_per_launch_int8_mfma": mfma_ops_launch, "ops_per_launch_algorithmic": ops[dom][0] / n_dom,
                      "avg_launch_ms": avg_launch_s * 1e3},
         "forward_mfma_frac": fwd_mfma_ops / (elapsed / args.steps) / PEAK_INT8_OPS,

@@ -618,7 +618,8 @@ int forward_impl(eii_model* m, const int64_t* ids, const std::vector<int32_t>& l
     max_T = std::max(max_T, (int)t);
   }
   if (M == 0) return EII_OK;
-  if (M > (size_t)INT32_MAX / kV) return fail(EII_E_ARG, "too many rows in one forward");
+  // every kernel indexes rows in size_t; the bound keeps row counts and tile counts in int
+  if (M > ((size_t)1 << 22)) return fail(EII_E_ARG, "more than 4194304 rows in one forward");
   if (max_T > m->rope_rows)
     return fail(EII_E_BOUND, "sequence of " + std::to_string(max_T) + " tokens exceeds the " +
                                  std::to_string(m->rope_rows) + " RoPE rows loaded (eii_model_set_rope)");

@@ -1,0 +1,234 @@
+"""Drop-in for python/intref.py backed by libeii on an MI355X.
+
+    sys.path.insert(0, "<repo>/exact-integer-inference_amd"); import intref
+    M = intref.Model(model_bin="model.bin")        # the file python/export_vectors.py writes
+    logits = M.forward(ids)                         # int64 [T, 49152], f = 16, bit-exact
+
+Same names, argument meanings and return types as python/intref.py (numpy int64 arrays in
+and out, AssertionError on violated bounds, ValueError for a request outside what the engine
+implements).  Differences, all deliberate:
+  * Model takes the weights from a model.bin instead of the safetensors checkpoint
+    (python/intref.py:132-151 quantizes those on load; model.bin is what that quantization
+    produces, python/export_vectors.py:24-45); `wide=False` (the comparison mode whose
+    formats model.bin does not record) raises.
+  * forward/embed/block/rmsnorm/linear/matmul_exact run on the GPU through libeii.so and
+    raise when it is missing; there is no CPU path.  rs, sat, dequant and the quantizers are
+    the reference's host-side elementwise helpers (its callers apply them to host arrays).
+  * block(..., trace) fills the trace keys the engine can dump (every activation site,
+    resid_in/resid_mid/resid_out); the reference's norm internals (_U, _z), attention
+    scores/probabilities and o_res/down_res/silu_gate are not produced.
+  * forward_batch(ids [B, T]) is an addition: B independent sequences in one call.
+"""
+import math
+import os
+
+import numpy as np
+
+from eii import modelbin as _mb
+from eii import tables as _tables
+
+F_RES = 15                        # python/intref.py:33-38
+F_SCORE = 7
+DMAX = 12 * 128
+EXP_BITS = 30
+EPS_S = 6184753
+R_ISQRT = 40
+I64 = np.int64
+
+
+def rs(x, n):                     # python/intref.py:42-50
+    if np.isscalar(n):
+        n = int(n)
+        if n <= 0:
+            return x << (-n)
+        return (x + (I64(1) << (n - 1))) >> n
+    n = np.asarray(n, dtype=I64)
+    assert (n >= 1).all(), "per-element shift must be >= 1"
+    return (x + (I64(1) << (n - 1))) >> n
+
+
+def sat(x, bits):                 # python/intref.py:53-55
+    lo, hi = -(1 << (bits - 1)), (1 << (bits - 1)) - 1
+    return np.clip(x, lo, hi)
+
+
+def dequant(q, f):                # python/intref.py:311
+    return np.asarray(q, dtype=np.float64) * 2.0 ** (-f)
+
+
+def exp_table():                  # python/intref.py:72-77
+    return _tables.exp_table()
+
+
+def silu_table(f_in, f_out, out_bits):   # python/intref.py:80-93
+    return _tables.silu_table(f_in, f_out, out_bits)
+
+
+def rope_tables(T, theta=100000, head_dim=64):   # python/intref.py:96-108
+    if theta != 100000 or head_dim != 64:
+        raise ValueError("the engine's RoPE is theta = 100000, head_dim = 64")
+    return _tables.rope_tables(T)
+
+
+def quant_rows(W):                # python/intref.py:113-124
+    """W float [N, K] -> (q int8-valued float64 [N, K], m int64 [N], n int64 [N]); scale m 2^-n."""
+    W = np.asarray(W, dtype=np.float64)
+    s = np.abs(W).max(1) / 127.0
+    s = np.where(s == 0, 1.0, s)
+    n = (13 - np.floor(np.log2(s))).astype(I64)
+    m = np.rint(s * 2.0 ** n).astype(I64)
+    assert m.min() >= 2 ** 13 and m.max() <= 2 ** 14
+    sw = m * 2.0 ** (-n.astype(np.float64))
+    return np.clip(np.rint(W / sw[:, None]), -127, 127), m, n
+
+
+def quant_vec_int16(w):           # python/intref.py:127-130
+    w = np.asarray(w, dtype=np.float64)
+    f = 14 - int(math.floor(math.log2(np.abs(w).max())))
+    return np.clip(np.rint(w * 2.0 ** f), -32768, 32767).astype(I64), f
+
+
+# ---------------------------------------------------------------- GPU operators
+
+def _torch():
+    import torch
+    if not torch.cuda.is_available():
+        from eii.lib import EIIError, EII_E_DEVICE
+        raise EIIError(EII_E_DEVICE, "intref: no GPU visible; this implementation runs only on the GPU")
+    return torch
+
+
+def _width(bound):
+    if bound <= 1 << 15:
+        return 16
+    if bound <= 1 << 31:
+        return 32
+    raise ValueError(f"activation bound {bound} exceeds the engine's 32-bit limb inputs")
+
+
+def _dev(a, dtype):
+    torch = _torch()
+    return torch.from_numpy(np.array(a, dtype=dtype, order="C")).cuda()
+
+
+def matmul_exact(A, Wf, bound_a, wmax=127):      # python/intref.py:58-63
+    """Exact int64 A [T, K] @ W [N, K]^T on the int8 MFMA path (int8-valued W, |A| <= 2^31)."""
+    import ctypes as C
+    from eii import lib as L
+    A = np.asarray(A)
+    K = A.shape[1]
+    assert bound_a * wmax * K < 2.0 ** 53, "float64 accumulation would not be exact"
+    W = np.asarray(Wf, dtype=np.float64)
+    if wmax > 127 or np.abs(W).max(initial=0) > 127 or np.any(W != np.rint(W)):
+        raise ValueError("matmul_exact on the engine needs int8 weights")
+    bits = _width(bound_a)
+    torch = _torch()
+    a = _dev(A, np.int16 if bits == 16 else np.int32)
+    w = _dev(W, np.int8)
+    N = W.shape[0]
+    pad = (-N) % 4                                   # the kernels take N in multiples of 4
+    if pad:
+        w = torch.cat([w, torch.zeros((pad, K), dtype=torch.int8, device=w.device)])
+    acc = torch.empty((A.shape[0], N + pad), dtype=torch.int64, device=w.device)
+    L.check(L.load().eii_gemm_i8(C.c_void_p(a.data_ptr()), bits, C.c_void_p(w.data_ptr()), A.shape[0], N + pad, K,
+                                 C.c_void_p(acc.data_ptr()), C.c_void_p(torch.cuda.current_stream().cuda_stream)))
+    return acc[:, :N].cpu().numpy()
+
+
+class Model:
+    """python/intref.py:132-301 over a model.bin held on one GPU."""
+
+    def __init__(self, wide=True, proposal_path=None, model_bin=None, device=0):
+        if not wide:
+            raise ValueError("narrow comparison mode is not recorded in model.bin")
+        path = model_bin or os.environ.get("EII_MODEL_BIN")
+        if not path:
+            raise ValueError("Model needs model_bin= (or EII_MODEL_BIN): the engine loads a model.bin")
+        from eii.engine import Engine
+        self.engine = Engine(path, device=device)
+        self.bin = _mb.read(path)
+        self.L = _mb.NL
+        self.wide = True
+        self.emb_q, self.emb_m, self.emb_n = self.bin.emb_q, self.bin.emb_m, self.bin.emb_n
+        self.final_gain = self.bin.final_gain
+        self.layers = [{k: L[k] for k in ("q", "k", "v", "o", "gate", "up", "down", "ln1", "ln2")}
+                       for L in self.bin.layers]
+        self.rope = (self.bin.rope_cos, self.bin.rope_sin)
+        self.f_y = self.bin.f_y
+
+    def fmt(self, site, l):                          # python/intref.py:154-160
+        if site == "final_out" and l == self.L:
+            return 16, self.f_y
+        return self.bin.fmt(site, l)
+
+    def embed(self, ids):                            # python/intref.py:163-166
+        return self.engine.embed(np.asarray(ids, dtype=I64)).cpu().numpy().astype(I64)
+
+    def rmsnorm(self, x, gain, f_out, bits_out, trace=None, tag=""):   # python/intref.py:168-184
+        import ctypes as C
+        from eii import lib as L
+        torch = _torch()
+        x = np.asarray(x)
+        assert x.shape[1] == _mb.D and x.min(initial=0) >= -2 ** 31 and x.max(initial=0) < 2 ** 31
+        wq, fw = gain
+        xd, gd = _dev(x, np.int32), _dev(wq, np.int32)
+        out = torch.empty(x.shape, dtype=torch.int16 if bits_out == 16 else torch.int32, device=xd.device)
+        L.check(L.load().eii_rmsnorm(C.c_void_p(xd.data_ptr()), x.shape[0], C.c_void_p(gd.data_ptr()), fw, f_out,
+                                     bits_out, C.c_void_p(out.data_ptr()),
+                                     C.c_void_p(torch.cuda.current_stream().cuda_stream)))
+        out = out.cpu().numpy().astype(I64)
+        if trace is not None:
+            trace[tag + "_out"] = out
+        return out
+
+    def linear(self, a, bound_a, W, f_in, f_out, bits_out):      # python/intref.py:186-190
+        import ctypes as C
+        from eii import lib as L
+        torch = _torch()
+        q, m, n = W
+        acc = matmul_exact(a, q, bound_a)
+        assert np.abs(acc).max(initial=0) * int(np.max(m)) < 2 ** 63
+        bits = _width(bound_a)
+        a_d = _dev(a, np.int16 if bits == 16 else np.int32)
+        w_d = _dev(q, np.int8)
+        N, K = w_d.shape
+        if N % 4:
+            raise ValueError("linear on the engine needs N a multiple of 4")
+        shift = np.asarray(n, dtype=I64) + f_in - f_out
+        assert (shift >= 1).all(), "per-element shift must be >= 1"
+        ws = torch.empty(N, dtype=torch.int32, device=w_d.device)
+        st = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+        lib = L.load()
+        L.check(lib.eii_weight_colsum(C.c_void_p(w_d.data_ptr()), N, K, C.c_void_p(ws.data_ptr()), st))
+        m_d, s_d = _dev(m, np.int32), _dev(shift, np.int32)
+        out = torch.empty((a_d.shape[0], N), dtype=torch.int16 if bits_out == 16 else torch.int32, device=w_d.device)
+        L.check(lib.eii_linear(C.c_void_p(a_d.data_ptr()), bits, C.c_void_p(w_d.data_ptr()), C.c_void_p(ws.data_ptr()),
+                               C.c_void_p(m_d.data_ptr()), C.c_void_p(s_d.data_ptr()), a_d.shape[0], N, K, bits_out,
+                               C.c_void_p(out.data_ptr()), st))
+        return out.cpu().numpy().astype(I64), acc
+
+    def block(self, l, x, trace=None):               # python/intref.py:192-286
+        torch = _torch()
+        x = np.asarray(x)
+        T = x.shape[0]
+        xd = _dev(x, np.int32)
+        if trace is not None:
+            trace["resid_in"] = x.copy()
+        bufs = self.engine.block(l, xd, 1, T, trace=trace is not None)
+        out = xd.cpu().numpy().astype(I64)
+        if trace is not None:
+            for k, v in bufs.items():
+                trace[k] = v.cpu().numpy().astype(I64)
+            trace["resid_out"] = out.copy()
+        return out
+
+    def forward(self, ids, narrow_residual=False):   # python/intref.py:288-301
+        if narrow_residual:
+            raise ValueError("narrow_residual is an ablation mode outside the engine")
+        ids = np.asarray(ids, dtype=I64).reshape(-1)
+        return self.forward_batch(ids[None, :])[0]
+
+    def forward_batch(self, ids):
+        """ids int64 [B, T] -> logits int64 [B, T, 49152]: B independent sequences."""
+        out = self.engine.forward(np.asarray(ids, dtype=I64), logits=True)
+        return out["logits"].cpu().numpy().astype(I64)

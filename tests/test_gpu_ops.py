@@ -121,6 +121,14 @@ def test_attention_ctx32(oracle):
     _attention_case(oracle, [100], scale=3000.0, seed=5, f_c=27, bits_c=32)
 
 
+@pytest.mark.parametrize("lens", [[33, 200], [45, 300], [700]])
+def test_attention_long(oracle, lens):
+    # sequences over 8 key tiles take the variant that recomputes scores per pass; starts that
+    # are not multiples of 32 exercise the masked first key tile
+    _attention_case(oracle, lens, scale=2000.0, seed=sum(lens))
+    _attention_case(oracle, lens, scale=20000.0, seed=sum(lens) + 1, f_qr=8, f_kr=8)
+
+
 @pytest.mark.parametrize("a_bits,out_bits,M,N,K", [(16, 16, 300, 192, 576), (16, 32, 37, 576, 576),
                                                     (32, 16, 130, 576, 1536), (32, 32, 64, 1536, 576),
                                                     (16, 16, 257, 3072, 576)])

@@ -69,12 +69,6 @@ __device__ __forceinline__ int32_t rne_i32(double y) {   // |y| < 2^31 after cla
 __device__ __forceinline__ double req2(int32_t P1, int32_t P0, double2 k) {
   return fma((double)P1 * 256.0, k.x, fma((double)P0, k.x, k.y));
 }
-// SAT(RS(x, sh), bits) for an integer-valued double x with |x| < 2^52 (scalar shift, any sign)
-__device__ __forceinline__ int32_t rs_sat_f64(double x, int sh, double lo, double hi) {
-  const double y = sh >= 1 ? fma(x, ldexp(1.0, -sh), ldexp(0.5, -sh)) : x * ldexp(1.0, -sh);
-  return rne_i32(fmin(fmax(y, lo), hi));
-}
-
 typedef int v16i __attribute__((ext_vector_type(16)));
 __device__ __forceinline__ v16i mfma32(v4i a, v4i b, v16i c) {
   return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
@@ -185,6 +179,207 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
 #pragma unroll
       for (int l = 0; l < AW; ++l) acc[a][b][l] = v16i{};
 
+  // Epilogue of tile (mb, nb).  Lane value (tm, tn, e) sits at tile row rw + 32 tm + roff(e)
+  // (rw = wm WM + 4 fh) and tile column cw + 32 tn (cw = wn WN + fc).  Addresses are 32-bit
+  // offsets from per-tile bases; loads are unconditional (rows past M read row M - 1) so they
+  // issue back to back, and only the stores test the row.
+  auto epilogue = [&](int mb, int nb) __attribute__((always_inline)) {
+    const int m0 = mb * C::BM, n0 = nb * C::BN;
+    const int rw = wm * C::WM + 4 * fh, cw = wn * C::WN + fc;
+    auto roff = [](int e) { return 8 * (e >> 2) + (e & 3); };
+    auto live = [&](int tm, int e) { return m0 + rw + 32 * tm + roff(e) < g.M; };
+    const int rlast = g.M - 1 - m0;   // last valid tile row
+    // the row stride passes through an empty asm so the per-element offsets are recomputed here
+    // instead of being hoisted out of the tile loop (64 loop-invariant offsets would spill)
+    int N = g.N;
+    __asm__ volatile("" : "+s"(N));
+    const int64_t bias = limb_bias(AW);
+    auto acc64 = [&](int tm, int tn, int e, int32_t ws) -> int64_t {
+      int64_t a = bias * (int64_t)ws;
+#pragma unroll
+      for (int l = 0; l < AW; ++l) a += (int64_t)acc[tm][tn][l][e] * ((int64_t)1 << (8 * l));
+      return a;
+    };
+
+    if constexpr (EPI == EPI_I64 || EPI == EPI_REQ16 || EPI == EPI_REQ32 || EPI == EPI_RESID || EPI == EPI_LOGITS) {
+      using OT = std::conditional_t<EPI == EPI_I64, int64_t, std::conditional_t<EPI == EPI_REQ16, int16_t, int32_t>>;
+      OT* tb = (OT*)g.out + (size_t)m0 * g.N + n0;
+      const double lo = EPI == EPI_REQ16 || EPI == EPI_REQ32 ? -ldexp(1.0, g.sat_bits - 1) : 0.0;
+      const double hi = EPI == EPI_REQ16 || EPI == EPI_REQ32 ? ldexp(1.0, g.sat_bits - 1) - 1.0 : 0.0;
+#pragma unroll
+      for (int tn = 0; tn < C::TN; ++tn) {
+        const int n = n0 + cw + 32 * tn;
+        if (n >= g.N) continue;
+        const int32_t ws = (AW == 4 || EPI == EPI_I64) ? g.wsum[n] : 0;
+        int32_t mu = 0, sh = 1;
+        double2 k = make_double2(0.0, 0.0);
+        if constexpr (AW == 4 && EPI != EPI_I64) { mu = g.mult[n]; sh = g.shift[n]; }
+        if constexpr (AW == 2 && EPI != EPI_I64) k = g.coef[n];
+        bool bad = false;
+#pragma unroll
+        for (int tm = 0; tm < C::TM; ++tm) {
+          const uint32_t o0 = (uint32_t)(rw + 32 * tm) * (uint32_t)N + (uint32_t)(cw + 32 * tn);
+          auto at = [&](int e) { return o0 + (uint32_t)(roff(e) * N); };
+          if constexpr (EPI == EPI_I64) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+              if (live(tm, e)) tb[at(e)] = acc64(tm, tn, e, ws);
+            continue;
+          }
+          // residual epilogue: the loads of 8 rows issue together, then their updates
+#pragma unroll
+          for (int eh = 0; eh < 16; eh += 8) {
+            int32_t xv[8];
+            if constexpr (EPI == EPI_RESID) {
+#pragma unroll
+              for (int i = 0; i < 8; ++i)
+                xv[i] = tb[(uint32_t)min(rw + 32 * tm + roff(eh + i), rlast) * (uint32_t)N + (uint32_t)(cw + 32 * tn)];
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+              const int e = eh + i;
+              // RS(acc * m, sh): exact integer-valued double + 2^-(sh+1) offset (2 limbs) or int64 (4 limbs)
+              double y = 0.0;
+              int64_t v = 0;
+              if constexpr (AW == 2) y = req2(acc[tm][tn][1][e], acc[tm][tn][0][e], k);
+              else v = rs(acc64(tm, tn, e, ws) * mu, sh);
+              int32_t q;
+              if constexpr (EPI == EPI_REQ16 || EPI == EPI_REQ32) {
+                q = AW == 2 ? rne_i32(fmin(fmax(y, lo), hi)) : (int32_t)sat(v, g.sat_bits);
+              } else if constexpr (EPI == EPI_RESID) {
+                q = AW == 2 ? rne_i32(fmin(fmax(rint(y) + (double)xv[i], -2147483648.0), 2147483647.0))
+                            : (int32_t)clamp_bits32((int64_t)xv[i] + v);
+              } else {   // EPI_LOGITS
+                if constexpr (AW == 2) {
+                  const double t2 = rint(y);
+                  bad |= t2 > 2147483647.0 || t2 < -2147483648.0;
+                  q = rne_i32(t2);
+                } else {
+                  bad |= v != (int64_t)(int32_t)v;
+                  q = (int32_t)v;
+                }
+              }
+              if (live(tm, e)) tb[at(e)] = (OT)q;
+            }
+          }
+        }
+        if constexpr (EPI == EPI_LOGITS) {
+          if (bad) atomicOr(g.flag, 1);
+        }
+      }
+    } else if (n0 + wn * C::WN < g.N) {
+      // columns c (tn = 0) and 32 + c (tn = 1) of the wave's 64-column block: (gate j, up j) for
+      // EPI_SILU (weight rows stacked as [gate 32 | up 32] blocks), (d, d + 32) of one head for EPI_QKV
+      const int nc = n0 + cw;
+      const double2 k0 = g.coef[nc], k1 = g.coef[nc + 32];
+      auto value16 = [&](int tm, int tn, int e) -> int32_t {   // SAT16(RS(acc * m, sh)) of column nc + 32 tn
+        if constexpr (AW == 2) {
+          return rne_i32(fmin(fmax(req2(acc[tm][tn][1][e], acc[tm][tn][0][e], tn ? k1 : k0), -32768.0), 32767.0));
+        } else {
+          const int n = nc + 32 * tn;
+          return (int32_t)clamp_bits16(rs(acc64(tm, tn, e, g.wsum[n]) * g.mult[n], g.shift[n]));
+        }
+      };
+      if constexpr (EPI == EPI_SILU) {
+        // gated limb planes [bits2 / 8][M][N / 2]; this lane's gated column is n0 / 2 + wn 32 + fc
+        const int NG = N / 2;
+        const double lo = -ldexp(1.0, g.bits2 - 1), hi = ldexp(1.0, g.bits2 - 1) - 1.0;
+        // RS(x, sh) = RNE(x 2^-sh + 2^-(sh+1)) for sh >= 1; for sh <= 0 the scaled value is an integer
+        const double sc = ldexp(1.0, -g.sh2), half = g.sh2 >= 1 ? ldexp(0.5, -g.sh2) : 0.0;
+        const size_t pl = (size_t)g.M * NG;
+        uint8_t* tb = (uint8_t*)g.out + (size_t)m0 * NG + n0 / 2;
+#pragma unroll
+        for (int tm = 0; tm < C::TM; ++tm) {
+          const uint32_t o0 = (uint32_t)(rw + 32 * tm) * (uint32_t)NG + (uint32_t)(wn * 32 + fc);
+          int32_t gv[16], uv[16], sv[16];
+#pragma unroll
+          for (int e = 0; e < 16; ++e) { gv[e] = value16(tm, 0, e); uv[e] = value16(tm, 1, e); }
+#pragma unroll
+          for (int e = 0; e < 16; ++e) sv[e] = g.aux_tab[gv[e] + 32768];   // the table gathers together
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            // SAT(RS(silu * up, sh2), bits2): the product and the scaled sum are exact in float64
+            const double x = (double)sv[e] * (double)uv[e];
+            const int32_t v = rne_i32(fmin(fmax(fma(x, sc, half), lo), hi));
+            if (!live(tm, e)) continue;
+            uint8_t* ob = tb + o0 + (uint32_t)(roff(e) * NG);
+            if (g.bits2 == 16) {
+              ob[0] = (uint8_t)limb_byte(v, 0, 2);
+              ob[pl] = (uint8_t)limb_byte(v, 1, 2);
+            } else {
+#pragma unroll
+              for (int l = 0; l < 4; ++l) ob[l * pl] = (uint8_t)limb_byte(v, l, 4);
+            }
+          }
+        }
+      } else {   // EPI_QKV: heads 0..8 q and 9..11 k get RoPE, 12..14 v are stored as they are
+        const int head = (n0 + wn * C::WN) >> 6;
+        int16_t* tb = (int16_t*)g.out + (size_t)m0 * g.N + n0;
+        if (head >= 12) {
+          // v: int16 rows and, when requested, the V^T limb planes (4 consecutive rows per dword;
+          // rows up to the tile end fit vt_stride, so no row test there)
+          const size_t vcol = (size_t)((head - 12) * 64 + fc) * g.vt_stride, vpl = (size_t)192 * g.vt_stride;
+#pragma unroll
+          for (int tm = 0; tm < C::TM; ++tm) {
+            const uint32_t o0 = (uint32_t)(rw + 32 * tm) * (uint32_t)N + (uint32_t)cw;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+              int32_t v1[4], v2[4];
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                const int e = 4 * b + r;
+                v1[r] = value16(tm, 0, e);
+                v2[r] = value16(tm, 1, e);
+                if (live(tm, e)) {
+                  int16_t* op = tb + o0 + (uint32_t)(roff(e) * N);
+                  op[0] = (int16_t)v1[r];
+                  op[32] = (int16_t)v2[r];
+                }
+              }
+              if (g.vt) {
+                uint8_t* vp = g.vt + vcol + (m0 + rw + 32 * tm + 8 * b);
+                const size_t d32 = (size_t)32 * g.vt_stride;
+                *(uint32_t*)vp = limb_word(v1, 0, 2);
+                *(uint32_t*)(vp + vpl) = limb_word(v1, 1, 2);
+                *(uint32_t*)(vp + d32) = limb_word(v2, 0, 2);
+                *(uint32_t*)(vp + d32 + vpl) = limb_word(v2, 1, 2);
+              }
+            }
+          }
+        } else {
+          const int shr = head < 9 ? g.sh_q : g.sh_k;
+          const double sc = ldexp(1.0, -shr), half = shr >= 1 ? ldexp(0.5, -shr) : 0.0;
+#pragma unroll
+          for (int tm = 0; tm < C::TM; ++tm) {
+            const uint32_t o0 = (uint32_t)(rw + 32 * tm) * (uint32_t)N + (uint32_t)cw;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+              int32_t cs[4], sn[4];
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                const int ps = g.pos[min(m0 + rw + 32 * tm + 8 * b + r, g.M - 1)];
+                cs[r] = g.cosT[ps * 32 + fc];
+                sn[r] = g.sinT[ps * 32 + fc];
+              }
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+              const int e = 4 * b + r;
+              const double a1 = (double)value16(tm, 0, e), a2 = (double)value16(tm, 1, e);
+              const double c = (double)cs[r], s2 = (double)sn[r];
+              const int32_t o1 = rne_i32(fmin(fmax(fma(fma(a1, c, -a2 * s2), sc, half), -32768.0), 32767.0));
+              const int32_t o2 = rne_i32(fmin(fmax(fma(fma(a2, c, a1 * s2), sc, half), -32768.0), 32767.0));
+              if (!live(tm, e)) continue;
+              int16_t* op = tb + o0 + (uint32_t)(roff(e) * N);
+              op[0] = (int16_t)o1;
+              op[32] = (int16_t)o2;
+              }
+            }
+          }
+        }
+      }
+    }
+  };
+
   // Step s computes from LDS stage s % 2 and weight register set s % 2; both were loaded two
   // steps earlier, the activations stored to LDS during step s - 1.  Every tile is unrolled
   // (two tiles per iteration when NK is odd), so the parity of each step is a compile-time
@@ -227,154 +422,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
     // ---------------------------------------------------------------- epilogue
     int mb, nb;
     tile_coords(v0 + jt * nwg_x, nMB, nNB, mb, nb);
-    const int mbase = mb * C::BM + wm * C::WM + 4 * fh;   // row of (tm, j) = mbase + 32 tm + 8 (j/4) + (j%4)
-    const int nblk = nb * C::BN + wn * C::WN;              // column of (tn) = nblk + 32 tn + fc
-    const int64_t bias = limb_bias(AW);
-    auto acc64 = [&](int tm, int tn, int e, int32_t ws) -> int64_t {
-      int64_t a = bias * (int64_t)ws;
-#pragma unroll
-      for (int l = 0; l < AW; ++l) a += (int64_t)acc[tm][tn][l][e] * ((int64_t)1 << (8 * l));
-      return a;
-    };
-    auto row_of = [&](int tm, int e) { return mbase + 32 * tm + 8 * (e >> 2) + (e & 3); };
-
-    if constexpr (EPI == EPI_I64 || EPI == EPI_REQ16 || EPI == EPI_REQ32 || EPI == EPI_RESID || EPI == EPI_LOGITS) {
-      const double lo = EPI == EPI_REQ16 || EPI == EPI_REQ32 ? -ldexp(1.0, g.sat_bits - 1) : 0.0;
-      const double hi = EPI == EPI_REQ16 || EPI == EPI_REQ32 ? ldexp(1.0, g.sat_bits - 1) - 1.0 : 0.0;
-#pragma unroll
-      for (int tn = 0; tn < C::TN; ++tn) {
-        const int n = nblk + 32 * tn + fc;
-        if (n >= g.N) continue;
-        const int32_t ws = (AW == 4 || EPI == EPI_I64) ? g.wsum[n] : 0;
-        int32_t mu = 0, sh = 1;
-        double2 k = make_double2(0.0, 0.0);
-        if constexpr (AW == 4 && EPI != EPI_I64) { mu = g.mult[n]; sh = g.shift[n]; }
-        if constexpr (AW == 2 && EPI != EPI_I64) k = g.coef[n];
-        bool bad = false;
-#pragma unroll
-        for (int tm = 0; tm < C::TM; ++tm)
-#pragma unroll
-          for (int e = 0; e < 16; ++e) {
-            const int m = row_of(tm, e);
-            if (m >= g.M) continue;
-            const size_t o = (size_t)m * g.N + n;
-            if constexpr (EPI == EPI_I64) {
-              ((int64_t*)g.out)[o] = acc64(tm, tn, e, ws);
-              continue;
-            }
-            // RS(acc * m, sh): exact integer-valued double + 2^-(sh+1) offset (2 limbs) or int64 (4 limbs)
-            double y = 0.0;
-            int64_t v = 0;
-            if constexpr (AW == 2) y = req2(acc[tm][tn][1][e], acc[tm][tn][0][e], k);
-            else v = rs(acc64(tm, tn, e, ws) * mu, sh);
-            if constexpr (EPI == EPI_REQ16 || EPI == EPI_REQ32) {
-              const int32_t q = AW == 2 ? rne_i32(fmin(fmax(y, lo), hi)) : (int32_t)sat(v, g.sat_bits);
-              if constexpr (EPI == EPI_REQ16) ((int16_t*)g.out)[o] = (int16_t)q;
-              else ((int32_t*)g.out)[o] = q;
-            } else if constexpr (EPI == EPI_RESID) {
-              int32_t* xp = (int32_t*)g.out + o;
-              const int32_t x = *xp;
-              *xp = AW == 2 ? rne_i32(fmin(fmax(rint(y) + (double)x, -2147483648.0), 2147483647.0))
-                            : (int32_t)clamp_bits32((int64_t)x + v);
-            } else {   // EPI_LOGITS
-              if constexpr (AW == 2) {
-                const double t2 = rint(y);
-                bad |= t2 > 2147483647.0 || t2 < -2147483648.0;
-                ((int32_t*)g.out)[o] = rne_i32(t2);
-              } else {
-                bad |= v != (int64_t)(int32_t)v;
-                ((int32_t*)g.out)[o] = (int32_t)v;
-              }
-            }
-          }
-        if constexpr (EPI == EPI_LOGITS) {
-          if (bad) atomicOr(g.flag, 1);
-        }
-      }
-    } else if (nblk < g.N) {
-      // columns c (tn = 0) and 32 + c (tn = 1) of the wave's 64-column block: (gate j, up j) for
-      // EPI_SILU (weight rows stacked as [gate 32 | up 32] blocks), (d, d + 32) of one head for EPI_QKV
-      const int nc = nblk + fc;
-      auto value16 = [&](int tm, int tn, int e, int n) -> int32_t {   // SAT16(RS(acc * m, sh)) of column n
-        if constexpr (AW == 2) {
-          return rne_i32(fmin(fmax(req2(acc[tm][tn][1][e], acc[tm][tn][0][e], g.coef[n]), -32768.0), 32767.0));
-        } else {
-          return (int32_t)clamp_bits16(rs(acc64(tm, tn, e, g.wsum[n]) * g.mult[n], g.shift[n]));
-        }
-      };
-      if constexpr (EPI == EPI_SILU) {
-        const double lo = -ldexp(1.0, g.bits2 - 1), hi = ldexp(1.0, g.bits2 - 1) - 1.0;
-        const int jg = (nblk >> 6) * 32 + fc;               // gated column
-        const size_t pl = (size_t)g.M * (g.N / 2);
-#pragma unroll
-        for (int tm = 0; tm < C::TM; ++tm)
-#pragma unroll
-          for (int e = 0; e < 16; ++e) {
-            const int m = row_of(tm, e);
-            if (m >= g.M) continue;
-            const int32_t gv = value16(tm, 0, e, nc), uv = value16(tm, 1, e, nc + 32);
-            const int32_t v = rs_sat_f64((double)g.aux_tab[gv + 32768] * (double)uv, g.sh2, lo, hi);
-            // gated limb planes [bits2 / 8][M][N / 2]
-            uint8_t* ob = (uint8_t*)g.out + (size_t)m * (g.N / 2) + jg;
-            if (g.bits2 == 16) {
-              ob[0] = (uint8_t)limb_byte(v, 0, 2);
-              ob[pl] = (uint8_t)limb_byte(v, 1, 2);
-            } else {
-#pragma unroll
-              for (int l = 0; l < 4; ++l) ob[l * pl] = (uint8_t)limb_byte(v, l, 4);
-            }
-          }
-      } else {   // EPI_QKV: heads 0..8 q and 9..11 k get RoPE, 12..14 v are stored as they are
-        const int head = nblk >> 6;
-        if (head >= 12) {
-          // v: int16 rows and, when requested, the V^T limb planes (4 consecutive rows per dword;
-          // rows up to the tile end fit vt_stride, so no row test there)
-          const size_t vcol = (size_t)((head - 12) * 64 + fc) * g.vt_stride, vpl = (size_t)192 * g.vt_stride;
-#pragma unroll
-          for (int tm = 0; tm < C::TM; ++tm)
-#pragma unroll
-            for (int b = 0; b < 4; ++b) {
-              int32_t v1[4], v2[4];
-#pragma unroll
-              for (int r = 0; r < 4; ++r) {
-                const int e = 4 * b + r, m = row_of(tm, e);
-                v1[r] = value16(tm, 0, e, nc);
-                v2[r] = value16(tm, 1, e, nc + 32);
-                if (m < g.M) {
-                  int16_t* op = (int16_t*)g.out + (size_t)m * g.N + nc;
-                  op[0] = (int16_t)v1[r];
-                  op[32] = (int16_t)v2[r];
-                }
-              }
-              if (g.vt) {
-                uint8_t* vp = g.vt + vcol + row_of(tm, 4 * b);
-                const size_t d32 = (size_t)32 * g.vt_stride;
-                *(uint32_t*)vp = limb_word(v1, 0, 2);
-                *(uint32_t*)(vp + vpl) = limb_word(v1, 1, 2);
-                *(uint32_t*)(vp + d32) = limb_word(v2, 0, 2);
-                *(uint32_t*)(vp + d32 + vpl) = limb_word(v2, 1, 2);
-              }
-            }
-        } else {
-          const int shr = head < 9 ? g.sh_q : g.sh_k;
-#pragma unroll
-          for (int tm = 0; tm < C::TM; ++tm)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-              const int m = row_of(tm, e);
-              if (m >= g.M) continue;
-              const int32_t a1 = value16(tm, 0, e, nc), a2 = value16(tm, 1, e, nc + 32);
-              const int ps = g.pos[m];
-              const double c = (double)g.cosT[ps * 32 + fc], sn = (double)g.sinT[ps * 32 + fc];
-              const int32_t o1 = rs_sat_f64(fma((double)a1, c, -(double)a2 * sn), shr, -32768.0, 32767.0);
-              const int32_t o2 = rs_sat_f64(fma((double)a2, c, (double)a1 * sn), shr, -32768.0, 32767.0);
-              int16_t* op = (int16_t*)g.out + (size_t)m * g.N + nc;
-              op[0] = (int16_t)o1;
-              op[32] = (int16_t)o2;
-            }
-        }
-      }
-    }
+    epilogue(mb, nb);
 #pragma unroll
     for (int a = 0; a < C::TM; ++a)
 #pragma unroll

@@ -41,12 +41,13 @@ const int kMatN[7] = {576, 192, 192, 576, 1536, 1536, 576};
 const int kMatK[7] = {576, 576, 576, 576, 576, 576, 1536};
 
 struct Mat {            // device arrays of one projection (possibly several matrices stacked)
-  int8_t* W = nullptr;  // [N, K]
+  int8_t* W = nullptr;  // [N, K] row-major (model arena)
   int32_t* mult = nullptr;
   int32_t* shift = nullptr;
   int32_t* wsum = nullptr;
   int N = 0, K = 0;
   double2* coef = nullptr;   // [N] float64 requantization coefficients for 2-limb inputs
+  int8_t* Wf = nullptr;      // the same weights in the GEMM's fragment order (kernels.h)
 };
 
 struct Layer {
@@ -77,6 +78,7 @@ struct Arena {
 struct eii_model {
   int device = 0;
   uint8_t* dev = nullptr;           // arena base
+  int8_t* wfrag = nullptr;          // fragment-ordered copies of every projection's weights
   // header arrays (device)
   int8_t* emb_q = nullptr;
   int32_t *emb_m = nullptr, *emb_sh = nullptr;   // embed shift n - 15
@@ -394,6 +396,25 @@ extern "C" int eii_model_load(const char* path, int device, eii_model** out) {
       if (e == hipSuccess) e = gemm_coef(m->mult, m->shift, m->wsum, m->N, m->coef, nullptr);
     }
   }
+  // fragment-ordered weights for the GEMMs (the arena keeps the row-major ones: the embedding
+  // lookup reads emb_q by row)
+  {
+    std::vector<Mat*> all{&M->head};
+    for (int l = 0; l < kNL; ++l) {
+      Layer& L = M->L[l];
+      all.insert(all.end(), {&L.qkv, &L.o, &L.gu, &L.down});
+    }
+    size_t total = 0;
+    for (Mat* m : all) total += (swizzled_bytes(m->N, m->K) + 255) & ~(size_t)255;
+    if (e == hipSuccess) e = hipMalloc(&M->wfrag, total);
+    size_t off = 0;
+    for (Mat* m : all) {
+      if (e != hipSuccess) break;
+      m->Wf = M->wfrag + off;
+      off += (swizzled_bytes(m->N, m->K) + 255) & ~(size_t)255;
+      e = swizzle_weights(m->W, m->N, m->K, m->Wf, nullptr);
+    }
+  }
   if (e == hipSuccess) e = hipMalloc(&M->flags, 16);
   if (e == hipSuccess) e = hipMemset(M->flags, 0, 16);
   if (e == hipSuccess) e = hipDeviceSynchronize();
@@ -419,6 +440,7 @@ extern "C" void eii_model_free(eii_model* m) {
   if (m->flags) (void)hipFree(m->flags);
   for (hipEvent_t e : m->ev) (void)hipEventDestroy(e);
   if (m->dev) (void)hipFree(m->dev);
+  if (m->wfrag) (void)hipFree(m->wfrag);
   delete m;
 }
 
@@ -507,7 +529,7 @@ int set_batch(eii_model* m, const std::vector<int32_t>& lens, hipStream_t s) {
 }
 
 GemmArgs gemm_args(const Mat& W, const void* planes, int M, void* out, int sat_bits) {
-  GemmArgs g{planes, W.W, M, W.N, W.K, (size_t)M * W.K, W.wsum, W.mult, W.shift, out, sat_bits, nullptr};
+  GemmArgs g{planes, W.Wf, M, W.N, W.K, (size_t)M * W.K, W.wsum, W.mult, W.shift, out, sat_bits, nullptr};
   g.coef = W.coef;
   return g;
 }
@@ -742,15 +764,25 @@ static int check_gemm_args(const void* A, int a_bits, const int8_t* W, int M, in
   return EII_OK;
 }
 
-// Splits plain A [M, K] into a stream-ordered temporary of limb planes (freed on the stream).
-static int split_temp(const void* A, int a_bits, int M, int K, uint8_t** planes, hipStream_t s) {
-  const size_t n = (size_t)M * K;
-  HIPCHK(hipMallocAsync((void**)planes, n * (a_bits / 8), s));
-  hipError_t e = split_limbs(A, a_bits / 8, n, *planes, s);
-  if (e != hipSuccess) {
-    (void)hipFreeAsync(*planes, s);
-    return fail(EII_E_DEVICE, std::string("limb split: ") + hipGetErrorString(e));
+// Stream-ordered temporaries for the operator entry points (freed on the stream after use):
+// plain A [M, K] split into K-blocked limb planes, row-major W [N, K] in fragment order.
+struct Operands {
+  uint8_t* planes = nullptr;
+  int8_t* wf = nullptr;
+  hipStream_t s = nullptr;
+  ~Operands() {
+    if (planes) (void)hipFreeAsync(planes, s);
+    if (wf) (void)hipFreeAsync(wf, s);
   }
+};
+
+static int stage_operands(const void* A, int a_bits, const int8_t* W, int M, int N, int K, Operands& o, hipStream_t s) {
+  o.s = s;
+  HIPCHK(hipMallocAsync((void**)&o.planes, (size_t)M * K * (a_bits / 8), s));
+  HIPCHK(hipMallocAsync((void**)&o.wf, swizzled_bytes(N, K), s));
+  hipError_t e = split_limbs(A, a_bits / 8, M, K, o.planes, s);
+  if (e == hipSuccess) e = swizzle_weights(W, N, K, o.wf, s);
+  if (e != hipSuccess) return fail(EII_E_DEVICE, std::string("operand staging: ") + hipGetErrorString(e));
   return EII_OK;
 }
 
@@ -761,11 +793,10 @@ extern "C" int eii_gemm_i8_ws(const void* A, int a_bits, const int8_t* W, const 
   if (!wsum || !acc) return fail(EII_E_ARG, "null output");
   if (N % 4) return fail(EII_E_ARG, "N must be a multiple of 4");
   hipStream_t s = (hipStream_t)stream;
-  uint8_t* planes = nullptr;
-  if ((rc = split_temp(A, a_bits, M, K, &planes, s))) return rc;
-  GemmArgs g{planes, W, M, N, K, (size_t)M * K, wsum, nullptr, nullptr, acc, 64, nullptr};
+  Operands op;
+  if ((rc = stage_operands(A, a_bits, W, M, N, K, op, s))) return rc;
+  GemmArgs g{op.planes, op.wf, M, N, K, (size_t)M * K, wsum, nullptr, nullptr, acc, 64, nullptr};
   hipError_t e = gemm(g, a_bits / 8, EPI_I64, s);
-  (void)hipFreeAsync(planes, s);
   if (e != hipSuccess) return fail(EII_E_DEVICE, std::string("eii_gemm_i8: ") + hipGetErrorString(e));
   return EII_OK;
 }
@@ -793,9 +824,9 @@ extern "C" int eii_linear(const void* A, int a_bits, const int8_t* W, const int3
   if (out_bits != 16 && out_bits != 32) return fail(EII_E_ARG, "out_bits must be 16 or 32");
   if (N % 4) return fail(EII_E_ARG, "N must be a multiple of 4");
   hipStream_t s = (hipStream_t)stream;
-  uint8_t* planes = nullptr;
-  if ((rc = split_temp(A, a_bits, M, K, &planes, s))) return rc;
-  GemmArgs g{planes, W, M, N, K, (size_t)M * K, wsum, mult, shift, out, out_bits, nullptr};
+  Operands op;
+  if ((rc = stage_operands(A, a_bits, W, M, N, K, op, s))) return rc;
+  GemmArgs g{op.planes, op.wf, M, N, K, (size_t)M * K, wsum, mult, shift, out, out_bits, nullptr};
   double2* coef = nullptr;
   hipError_t e = hipSuccess;
   if (a_bits == 16) {
@@ -805,7 +836,6 @@ extern "C" int eii_linear(const void* A, int a_bits, const int8_t* W, const int3
   }
   if (e == hipSuccess) e = gemm(g, a_bits / 8, out_bits == 16 ? EPI_REQ16 : EPI_REQ32, s);
   if (coef) (void)hipFreeAsync(coef, s);
-  (void)hipFreeAsync(planes, s);
   if (e != hipSuccess) return fail(EII_E_DEVICE, std::string("eii_linear: ") + hipGetErrorString(e));
   return EII_OK;
 }

@@ -21,10 +21,22 @@ enum Epi : int {
 };
 
 // Activations enter the GEMM as int8 limb planes (eii_int.h split_limbs): a_bytes planes of
-// [M, K] bytes, plane l at A + l * a_plane, lowest byte first.
+// M x K bytes, plane l at A + l * a_plane, lowest byte first, each plane K-blocked: element
+// (m, k) at byte plane_offset(m, k, M), i.e. [K / 64][M][64], so the 64-byte K slices of
+// consecutive rows are contiguous.
+__host__ __device__ inline size_t plane_offset(size_t m, size_t k, size_t M) {
+  return (k >> 6) * M * 64 + m * 64 + (k & 63);
+}
+// Weights enter the GEMM in MFMA fragment order (swizzle_weights): for each block of 32 output
+// rows and each 32-column K slice, the 64 lanes' 16-byte operands in lane order,
+// [ceil(N / 32)][K / 32][64][16] (lane 32 h + c: row 32 b + c, columns 16 h .. 16 h + 15 of
+// the slice); rows past N are zero.
+inline size_t swizzled_bytes(int N, int K) { return (size_t)((N + 31) / 32) * 32 * K; }
+hipError_t swizzle_weights(const int8_t* W, int N, int K, int8_t* Wf, hipStream_t s);
+
 struct GemmArgs {
   const void* A;          // limb planes of the [M, K] activations, 2 (16-bit) or 4 (32-bit) planes
-  const int8_t* W;        // weights [N, K], row = output channel
+  const int8_t* W;        // weights [N, K] (row = output channel) in fragment order
   int M, N, K;            // K % 64 == 0
   size_t a_plane;         // bytes between limb planes (M * K for a dense [L][M][K] layout)
   const int32_t* wsum;    // [N] sum_k W[n, k]
@@ -66,13 +78,13 @@ hipError_t gemm_coef(const int32_t* mult, const int32_t* shift, const int32_t* w
 hipError_t embed(const int64_t* ids, int M, const int8_t* emb_q, const int32_t* emb_m,
                  const int32_t* emb_sh, int32_t* x, int* flag, hipStream_t s);
 
-// out = SAT(RS(3 * RS(x * U, 16) * gain, sh_out), bits_out) as limb planes [bits/8][M][576]
-// and/or plain int16/int32 [M, 576] (either pointer may be null)
+// out = SAT(RS(3 * RS(x * U, 16) * gain, sh_out), bits_out) as limb planes (bits/8 planes of
+// M x 576, K-blocked) and/or plain int16/int32 [M, 576] (either pointer may be null)
 hipError_t rmsnorm(const int32_t* x, int M, const int32_t* gain, int sh_out, int bits_out,
                    uint8_t* planes, void* plain, hipStream_t s);
 
-// n values int16 (a_bytes 2) or int32 (a_bytes 4) -> limb planes [a_bytes][n]
-hipError_t split_limbs(const void* a, int a_bytes, size_t n, uint8_t* planes, hipStream_t s);
+// plain [M, K] int16 (a_bytes 2) or int32 (a_bytes 4), K % 64 == 0 -> K-blocked limb planes
+hipError_t split_limbs(const void* a, int a_bytes, int M, int K, uint8_t* planes, hipStream_t s);
 
 // In-place rotate-half RoPE on the q (cols 0..575) and k (cols 576..767) parts of qkv [M, 960]
 hipError_t rope(int16_t* qkv, int M, const int32_t* pos, const int32_t* cosT, const int32_t* sinT,
@@ -89,7 +101,7 @@ struct AttnArgs {
   const int32_t* seq_off;  // [B + 1] row offsets of the sequences
   const int32_t* exp_tab;  // [1537]
   void* ctx;               // plain [M, 576], int16 or int32, or null
-  uint8_t* ctx_planes;     // limb planes [bits_c/8][M][576], or null
+  uint8_t* ctx_planes;     // K-blocked limb planes (bits_c/8 planes of M x 576), or null
   int M;
   int B, max_T;
   int max_kt;              // max over sequences of the 32-row key tiles it spans (attn_key_tiles)

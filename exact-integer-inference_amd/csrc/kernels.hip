@@ -123,8 +123,12 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
 
   // Load cursor: tile and K block of the next step to load, with this thread's source pointers
   // for that tile (advanced incrementally; divisions happen once per tile).  Rows past M and
-  // columns past N read row M - 1 / N - 1; their results are never stored.
+  // column blocks past N read row M - 1 / the last block; their results are never stored.
+  // Both operands are laid out so that each wave load instruction reads contiguous 1 KB runs:
+  // K-blocked activation planes (16 rows x 64 bytes) and fragment-ordered weights.
   int l_tile = 0, l_kb = 0;
+  const size_t a_kstep = (size_t)g.M * 64;              // activation bytes between K blocks
+  const int nb32_last = (g.N + 31) / 32 - 1;
   const uint8_t* a_src[C::kAChunks];
   const int8_t* w_src[C::TN];
   auto set_load_tile = [&](int j) __attribute__((always_inline)) {
@@ -136,26 +140,28 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
       // chunk q: limb plane l, row, 16-byte chunk c
       const int q = tid + C::kThreads * i, l = q / (4 * C::BM), row = (q >> 2) % C::BM, c = q & 3;
       const int m = min(m0 + row, g.M - 1);
-      a_src[i] = Ab + (size_t)l * g.a_plane + (size_t)m * g.K + c * 16;
+      a_src[i] = Ab + (size_t)l * g.a_plane + (size_t)m * 64 + c * 16;
     }
 #pragma unroll
     for (int tn = 0; tn < C::TN; ++tn) {
-      // this lane's B fragment: weight row n0 + 64 wn + 32 tn + c, K bytes 16 h of each 32-step
-      const int n = min(n0 + wn * C::WN + 32 * tn + fc, g.N - 1);
-      w_src[tn] = g.W + (size_t)n * g.K + 16 * fh;
+      // this lane's B fragments: weight rows n0 + 64 wn + 32 tn + 0..31, the lane's 16 bytes of
+      // each 32-column K slice
+      const int nb32 = min((n0 + wn * C::WN + 32 * tn) >> 5, nb32_last);
+      w_src[tn] = g.W + (size_t)nb32 * (g.K / 32) * 1024 + lane * 16;
     }
   };
   u32x4 areg[2][C::kAChunks];
   v4i wreg[2][C::TN][2];
   auto load = [&](auto SET) __attribute__((always_inline)) {   // the step at the cursor, into register set SET (compile time)
     constexpr int set = decltype(SET)::value;
-    const int kw = l_kb * kBK;
+    const size_t ka = (size_t)l_kb * a_kstep;
+    const int kw = l_kb * 2048;
 #pragma unroll
-    for (int i = 0; i < C::kAChunks; ++i) areg[set][i] = *(const u32x4*)(a_src[i] + kw);
+    for (int i = 0; i < C::kAChunks; ++i) areg[set][i] = *(const u32x4*)(a_src[i] + ka);
 #pragma unroll
     for (int tn = 0; tn < C::TN; ++tn)
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) wreg[set][tn][ks] = *(const v4i*)(w_src[tn] + kw + 32 * ks);
+      for (int ks = 0; ks < 2; ++ks) wreg[set][tn][ks] = *(const v4i*)(w_src[tn] + kw + 1024 * ks);
     if (++l_kb == nk) {
       l_kb = 0;
       if (++l_tile < ntiles) set_load_tile(l_tile);
@@ -281,16 +287,17 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
         }
       };
       if constexpr (EPI == EPI_SILU) {
-        // gated limb planes [bits2 / 8][M][N / 2]; this lane's gated column is n0 / 2 + wn 32 + fc
+        // gated limb planes (bits2 / 8 planes of M x N / 2, K-blocked): the lane's gated column
+        // n0 / 2 + wn 32 + fc lies in 64-column block nb at offset wn 32 + fc
         const int NG = N / 2;
         const double lo = -ldexp(1.0, g.bits2 - 1), hi = ldexp(1.0, g.bits2 - 1) - 1.0;
         // RS(x, sh) = RNE(x 2^-sh + 2^-(sh+1)) for sh >= 1; for sh <= 0 the scaled value is an integer
         const double sc = ldexp(1.0, -g.sh2), half = g.sh2 >= 1 ? ldexp(0.5, -g.sh2) : 0.0;
         const size_t pl = (size_t)g.M * NG;
-        uint8_t* tb = (uint8_t*)g.out + (size_t)m0 * NG + n0 / 2;
+        uint8_t* tb = (uint8_t*)g.out + (size_t)nb * g.M * 64 + (size_t)m0 * 64;
 #pragma unroll
         for (int tm = 0; tm < C::TM; ++tm) {
-          const uint32_t o0 = (uint32_t)(rw + 32 * tm) * (uint32_t)NG + (uint32_t)(wn * 32 + fc);
+          const uint32_t o0 = (uint32_t)(rw + 32 * tm) * 64u + (uint32_t)(wn * 32 + fc);
           int32_t gv[16], uv[16], sv[16];
 #pragma unroll
           for (int e = 0; e < 16; ++e) { gv[e] = value16(tm, 0, e); uv[e] = value16(tm, 1, e); }
@@ -302,7 +309,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
             const double x = (double)sv[e] * (double)uv[e];
             const int32_t v = rne_i32(fmin(fmax(fma(x, sc, half), lo), hi));
             if (!live(tm, e)) continue;
-            uint8_t* ob = tb + o0 + (uint32_t)(roff(e) * NG);
+            uint8_t* ob = tb + o0 + (uint32_t)(roff(e) * 64);
             if (g.bits2 == 16) {
               ob[0] = (uint8_t)limb_byte(v, 0, 2);
               ob[pl] = (uint8_t)limb_byte(v, 1, 2);
@@ -486,18 +493,28 @@ hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
 }
 
 template <int W>
-__global__ __launch_bounds__(256) void split_kernel(const void* a, size_t n, uint8_t* planes) {
-  const size_t i = ((size_t)blockIdx.x * 256 + threadIdx.x) * 4;   // 4 consecutive elements
+__global__ __launch_bounds__(256) void split_kernel(const void* a, int M, int K, uint8_t* planes) {
+  const size_t i = ((size_t)blockIdx.x * 256 + threadIdx.x) * 4;   // 4 consecutive elements of a row
+  const size_t n = (size_t)M * K;
   if (i >= n) return;
+  const size_t m = i / K, k = i % K;
   int32_t v[4];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) v[e] = i + e < n ? (W == 2 ? ((const int16_t*)a)[i + e] : ((const int32_t*)a)[i + e]) : 0;
+  for (int e = 0; e < 4; ++e) v[e] = W == 2 ? ((const int16_t*)a)[i + e] : ((const int32_t*)a)[i + e];
 #pragma unroll
-  for (int l = 0; l < W; ++l) {
-    const uint32_t w = limb_word(v, l, W);
-    if (i + 4 <= n) *(uint32_t*)(planes + l * n + i) = w;
-    else for (size_t e = 0; i + e < n; ++e) planes[l * n + i + e] = (uint8_t)(w >> (8 * e));
-  }
+  for (int l = 0; l < W; ++l) *(uint32_t*)(planes + l * n + plane_offset(m, k, M)) = limb_word(v, l, W);
+}
+
+// Weights [N, K] row-major -> fragment order (kernels.h swizzle_weights): thread = 16 bytes
+__global__ __launch_bounds__(256) void swizzle_kernel(const int8_t* W, int N, int K, int8_t* Wf) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x, ks = K / 32;
+  if (i >= (size_t)((N + 31) / 32) * ks * 64) return;
+  const int lane = (int)(i & 63);
+  const size_t kc = (i >> 6) % ks, nb = (i >> 6) / ks;
+  const size_t n = nb * 32 + (lane & 31), k = kc * 32 + 16 * (lane >> 5);
+  uint4 v = make_uint4(0, 0, 0, 0);
+  if (n < (size_t)N) v = *(const uint4*)(W + n * K + k);
+  *(uint4*)(Wf + i * 16) = v;
 }
 
 __global__ __launch_bounds__(256) void coef_kernel(const int32_t* mult, const int32_t* shift, const int32_t* wsum,
@@ -568,7 +585,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const int32_t* x, int M, c
     const int32_t o = (int32_t)sat(rs(z * gain[c] * 3, sh_out), bits_out);
     if (planes) {
 #pragma unroll
-      for (int l = 0; l < OB; ++l) planes[l * pl + e] = (uint8_t)limb_byte(o, l, OB);
+      for (int l = 0; l < OB; ++l) planes[l * pl + plane_offset(row, c, M)] = (uint8_t)limb_byte(o, l, OB);
     }
     if (plain) {
       if constexpr (OB == 2) ((int16_t*)plain)[e] = (int16_t)o;
@@ -608,7 +625,7 @@ __global__ __launch_bounds__(256) void silu_kernel(const int16_t* gu, int M, con
   const int32_t o = (int32_t)sat(rs((int64_t)silu[g + 32768] * u, sh), bits);
   if (planes) {
 #pragma unroll
-    for (int l = 0; l < OB; ++l) planes[l * (size_t)M * kDFF + t] = (uint8_t)limb_byte(o, l, OB);
+    for (int l = 0; l < OB; ++l) planes[l * (size_t)M * kDFF + plane_offset(row, j, M)] = (uint8_t)limb_byte(o, l, OB);
   }
   if (plain) {
     if constexpr (OB == 2) ((int16_t*)plain)[t] = (int16_t)o;
@@ -910,7 +927,8 @@ __global__ __launch_bounds__(192) void attn_kernel(AttnArgs a) {
       const int d0 = 32 * dt + 8 * b + 4 * h;
       if (a.ctx_planes) {
 #pragma unroll
-        for (int l = 0; l < OB; ++l) *(uint32_t*)(a.ctx_planes + l * pl + orow + d0) = limb_word(cv, l, OB);
+        for (int l = 0; l < OB; ++l)
+          *(uint32_t*)(a.ctx_planes + l * pl + plane_offset(qi, hh * 64 + d0, a.M)) = limb_word(cv, l, OB);
       }
       if (a.ctx) {
         if constexpr (OB == 2) *(uint2*)((int16_t*)a.ctx + orow + d0) = make_uint2(pack16(cv[0], cv[1]), pack16(cv[2], cv[3]));
@@ -981,10 +999,18 @@ hipError_t rmsnorm(const int32_t* x, int M, const int32_t* gain, int sh_out, int
   return hipGetLastError();
 }
 
-hipError_t split_limbs(const void* a, int a_bytes, size_t n, uint8_t* planes, hipStream_t s) {
-  dim3 grid((unsigned)((n / 4 + 256) / 256));
-  if (a_bytes == 2) hipLaunchKernelGGL(split_kernel<2>, grid, dim3(256), 0, s, a, n, planes);
-  else hipLaunchKernelGGL(split_kernel<4>, grid, dim3(256), 0, s, a, n, planes);
+hipError_t split_limbs(const void* a, int a_bytes, int M, int K, uint8_t* planes, hipStream_t s) {
+  if (K % 64 != 0) return hipErrorInvalidValue;
+  dim3 grid(blocks_for((size_t)M * K / 4));
+  if (a_bytes == 2) hipLaunchKernelGGL(split_kernel<2>, grid, dim3(256), 0, s, a, M, K, planes);
+  else hipLaunchKernelGGL(split_kernel<4>, grid, dim3(256), 0, s, a, M, K, planes);
+  return hipGetLastError();
+}
+
+hipError_t swizzle_weights(const int8_t* W, int N, int K, int8_t* Wf, hipStream_t s) {
+  if (K % 32 != 0 || N <= 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(swizzle_kernel, dim3(blocks_for((size_t)((N + 31) / 32) * (K / 32) * 64)), dim3(256), 0, s, W, N,
+                     K, Wf);
   return hipGetLastError();
 }
 

@@ -50,7 +50,7 @@ EII_HD int64_t clamp_bits32(int64_t x) {
 // float64 estimate of 2^40 / sqrt(Tt) is within one unit of U (relative error below 2^-48 on a
 // value below 2^29); the integer loops below then move u to the unique integer with
 //   u^2 * Tt <= 2^80 < (u + 1)^2 * Tt,
-// evaluated exactly in 128-bit arithmetic.
+// evaluated exactly with 64 x 64 -> 128-bit products.
 typedef unsigned __int128 u128;
 
 EII_HD u128 norm_total(int64_t A, int64_t B, int64_t C) {
@@ -59,25 +59,32 @@ EII_HD u128 norm_total(int64_t A, int64_t B, int64_t C) {
   return (u128)(S + kEpsS);
 }
 
+#if defined(__HIPCC__)
+EII_HD uint64_t umulhi64(uint64_t a, uint64_t b) { return __umul64hi(a, b); }
+#else
+EII_HD uint64_t umulhi64(uint64_t a, uint64_t b) { return (uint64_t)(((u128)a * b) >> 64); }
+#endif
+
+// u^2 * Tt <= 2^80 for u < 2^31 and Tt = t_hi 2^64 + t_lo < 2^74, in 64-bit pieces:
+// p Tt = p t_hi 2^64 + p t_lo with p = u^2 < 2^62.
 EII_HD bool norm_fits(uint64_t u, u128 Tt) {
-  // u^2 * Tt <= 2^80, for u < 2^31 (u^2 < 2^62) and Tt < 2^74.
-  const u128 p = (u128)u * (u128)u;
+  const uint64_t p = u * u;
   const uint64_t t_hi = (uint64_t)(Tt >> 64), t_lo = (uint64_t)Tt;
-  // p * Tt = p * t_lo + (p * t_hi) << 64; compare the part above 2^64 with 2^16.
-  const u128 a = p * (u128)t_lo;                 // < 2^126
-  const u128 b = p * (u128)t_hi;                 // < 2^72
-  const u128 top = b + (a >> 64);                // the product divided by 2^64, rounded down
-  if (top > ((u128)1 << 16)) return false;
-  if (top < ((u128)1 << 16)) return true;
-  return (uint64_t)a == 0;
+  const uint64_t ph = p * t_hi;
+  if (umulhi64(p, t_hi) != 0 || ph > ((uint64_t)1 << 16)) return false;   // p t_hi 2^64 > 2^80
+  const uint64_t top = ph + umulhi64(p, t_lo);                              // floor(p Tt / 2^64)
+  if (top != ((uint64_t)1 << 16)) return top < ((uint64_t)1 << 16);
+  return p * t_lo == 0;
 }
 
+// The float64 estimate is within one of U (see above), so U is u - 1, u or u + 1 for
+// u = floor(estimate); the loops also cover any larger miss.
 EII_HD int64_t norm_U(u128 Tt) {
   const double td = (double)(uint64_t)(Tt >> 64) * 18446744073709551616.0 + (double)(uint64_t)Tt;
   double ue = 1099511627776.0 / sqrt(td);           // 2^40 / sqrt(Tt)
   if (ue > 2147483647.0) ue = 2147483647.0;
   uint64_t u = (uint64_t)ue;
-  for (int it = 0; it < 64 && !norm_fits(u, Tt); ++it) --u;
+  for (int it = 0; it < 64 && u > 0 && !norm_fits(u, Tt); ++it) --u;
   for (int it = 0; it < 64 && norm_fits(u + 1, Tt); ++it) ++u;
   return (int64_t)u;
 }

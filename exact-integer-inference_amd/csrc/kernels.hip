@@ -556,40 +556,65 @@ __global__ __launch_bounds__(256) void embed_kernel(const int64_t* ids, int M, c
 }
 
 // ------------------------------------------------------------------------------ rmsnorm
-// One wave per row; lane j holds elements j, j+64, ..., j+512.
+// One wave per row; lane j holds elements j, j+64, ..., j+512.  Every product is a 32 x 32 -> 64
+// bit multiply-add: the squares through the 16-bit halves of x (python/intref.py:170-172),
+// z = RS(x U, 16) with U < 2^29 and |z| <= 2^24 (|x U| <= 2^40 since |x| <= sqrt(S)), then
+// 3 z gain with |3 z gain| < 2^41.  For output shifts in [10, 40] the shifted value fits int32
+// and saturates with one clamp; other shifts take the general int64 path.
 template <int OB>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const int32_t* x, int M, const int32_t* gain,
                                                       int sh_out, int bits_out, uint8_t* planes, void* plain) {
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
   if (row >= M) return;
   const int32_t* xr = x + (size_t)row * kD;
-  int32_t v[9];
+  int32_t v[9], g3[9];
   int64_t A = 0, B = 0, Cs = 0;
 #pragma unroll
   for (int j = 0; j < 9; ++j) {
     v[j] = xr[lane + 64 * j];
-    const int64_t hi = v[j] >> 16, lo = v[j] & 0xFFFF;
-    A += hi * hi; B += hi * lo; Cs += lo * lo;
+    g3[j] = gain[lane + 64 * j];
+  }
+#pragma unroll
+  for (int j = 0; j < 9; ++j) {
+    const int32_t hi = v[j] >> 16, lo = v[j] & 0xFFFF;
+    A += (int64_t)hi * hi; B += (int64_t)hi * lo; Cs += (int64_t)lo * lo;
+    g3[j] *= 3;
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
     A += __shfl_xor(A, o); B += __shfl_xor(B, o); Cs += __shfl_xor(Cs, o);
   }
-  const int64_t U = norm_U(norm_total(A, B, Cs));
-  const size_t pl = (size_t)M * kD;
+  const int32_t U = (int32_t)norm_U(norm_total(A, B, Cs));   // < 2^29
+  int32_t o[9];
+  if (sh_out >= 10 && sh_out <= 40) {
+    const int64_t rnd = (int64_t)1 << (sh_out - 1);
 #pragma unroll
-  for (int j = 0; j < 9; ++j) {
-    const int c = lane + 64 * j;
-    const size_t e = (size_t)row * kD + c;
-    const int64_t z = rs((int64_t)v[j] * U, 16);
-    const int32_t o = (int32_t)sat(rs(z * gain[c] * 3, sh_out), bits_out);
-    if (planes) {
-#pragma unroll
-      for (int l = 0; l < OB; ++l) planes[l * pl + plane_offset(row, c, M)] = (uint8_t)limb_byte(o, l, OB);
+    for (int j = 0; j < 9; ++j) {
+      const int32_t z = (int32_t)(((int64_t)v[j] * U + 32768) >> 16);
+      const int32_t q = (int32_t)(((int64_t)z * g3[j] + rnd) >> sh_out);
+      o[j] = OB == 2 ? min(max(q, -32768), 32767) : q;
     }
-    if (plain) {
-      if constexpr (OB == 2) ((int16_t*)plain)[e] = (int16_t)o;
-      else ((int32_t*)plain)[e] = o;
+  } else {
+#pragma unroll
+    for (int j = 0; j < 9; ++j) {
+      const int32_t z = (int32_t)(((int64_t)v[j] * U + 32768) >> 16);
+      o[j] = (int32_t)sat(rs((int64_t)z * g3[j], sh_out), bits_out);
+    }
+  }
+  if (planes) {   // K-blocked planes: element (row, lane + 64 j) at j M 64 + row 64 + lane
+    uint8_t* pb = planes + (size_t)row * 64 + lane;
+    const size_t pl = (size_t)M * kD, m64 = (size_t)M * 64;
+#pragma unroll
+    for (int j = 0; j < 9; ++j)
+#pragma unroll
+      for (int l = 0; l < OB; ++l) pb[l * pl + j * m64] = (uint8_t)limb_byte(o[j], l, OB);
+  }
+  if (plain) {
+#pragma unroll
+    for (int j = 0; j < 9; ++j) {
+      const size_t e = (size_t)row * kD + lane + 64 * j;
+      if constexpr (OB == 2) ((int16_t*)plain)[e] = (int16_t)o[j];
+      else ((int32_t*)plain)[e] = o[j];
     }
   }
 }

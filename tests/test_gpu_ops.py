@@ -75,7 +75,9 @@ def test_rmsnorm(oracle):
     x[5] = rng.integers(-2 ** 16, 2 ** 16, size=576)
     gain = rng.integers(-2 ** 15, 2 ** 15, size=576, dtype=np.int64)
     xt, gt = dev(x.astype(np.int32)), dev(gain.astype(np.int32))
-    for f_gain, f_out, bits in [(14, 13, 16), (14, 11, 16), (12, 20, 32), (14, 40, 16)]:
+    # shifts 22, 24, 13, 10 (fast path edge), -5, 7 and 41 (general path)
+    for f_gain, f_out, bits in [(14, 13, 16), (14, 11, 16), (12, 20, 32), (14, 25, 32), (14, 40, 16), (14, 28, 32),
+                                (20, 0, 16)]:
         want = oracle.rmsnorm(x, (gain, f_gain), f_out, bits)
         out = torch.empty((37, 576), dtype=torch.int16 if bits == 16 else torch.int32, device="cuda")
         L.check(lib.eii_rmsnorm(p(xt), 37, p(gt), f_gain, f_out, bits, p(out), None))

@@ -1,6 +1,7 @@
-"""Build libeii.so (gfx950 HIP kernels + C ABI) and libeii_hostcheck.so in place.
+"""Build libeii.so (gfx950 HIP kernels + C ABI), the eii_check conformance checker and
+libeii_hostcheck.so in place.
 
-    python build.py            # both libraries, next to this file
+    python build.py            # everything, next to this file
 """
 import os
 import subprocess
@@ -16,6 +17,7 @@ HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall",
              "-I" + CSRC, "-I" + INCLUDE]
 
 LIB = os.path.join(HERE, "libeii.so")
+CHECKER = os.path.join(HERE, "eii_check")
 HOSTCHECK = os.path.join(HERE, "libeii_hostcheck.so")
 
 
@@ -35,6 +37,12 @@ def build_lib():
     os.replace(LIB + ".tmp", LIB)
 
 
+def build_checker():
+    run([HIPCC, "-O2", "-std=c++17", "-Wall", "-I" + INCLUDE, os.path.join(CSRC, "eii_check.cpp"),
+         "-L" + HERE, "-leii", "-Wl,-rpath,$ORIGIN", "-o", CHECKER + ".tmp"])
+    os.replace(CHECKER + ".tmp", CHECKER)
+
+
 def build_hostcheck():
     run(["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-I" + CSRC,
          os.path.join(CSRC, "hostcheck.cpp"), "-o", HOSTCHECK])
@@ -42,6 +50,7 @@ def build_hostcheck():
 
 def build():
     build_lib()
+    build_checker()
     build_hostcheck()
 
 

@@ -66,8 +66,9 @@ __device__ __forceinline__ int32_t rne_i32(double y) {   // |y| < 2^31 after cla
 // Per-column coefficients for 2-limb inputs, precomputed once per weight matrix (coef_kernel):
 //   c0 = m 2^-sh,  cb = 128 wsum m 2^-sh + 2^-(sh+1).
 // acc * m / 2^sh + 2^-(sh+1) for acc = 256 P1 + P0 + 128 wsum (exact, see above):
-__device__ __forceinline__ double req2(int32_t P1, int32_t P0, double2 k) {
-  return fma((double)P1 * 256.0, k.x, fma((double)P0, k.x, k.y));
+// c1 = 256 c0, formed once per column.
+__device__ __forceinline__ double req2(int32_t P1, int32_t P0, double c1, double2 k) {
+  return fma((double)P1, c1, fma((double)P0, k.x, k.y));
 }
 typedef int v16i __attribute__((ext_vector_type(16)));
 __device__ __forceinline__ v16i mfma32(v4i a, v4i b, v16i c) {
@@ -221,6 +222,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
         double2 k = make_double2(0.0, 0.0);
         if constexpr (AW == 4 && EPI != EPI_I64) { mu = g.mult[n]; sh = g.shift[n]; }
         if constexpr (AW == 2 && EPI != EPI_I64) k = g.coef[n];
+        const double c1 = 256.0 * k.x;
         bool bad = false;
 #pragma unroll
         for (int tm = 0; tm < C::TM; ++tm) {
@@ -247,7 +249,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
               // RS(acc * m, sh): exact integer-valued double + 2^-(sh+1) offset (2 limbs) or int64 (4 limbs)
               double y = 0.0;
               int64_t v = 0;
-              if constexpr (AW == 2) y = req2(acc[tm][tn][1][e], acc[tm][tn][0][e], k);
+              if constexpr (AW == 2) y = req2(acc[tm][tn][1][e], acc[tm][tn][0][e], c1, k);
               else v = rs(acc64(tm, tn, e, ws) * mu, sh);
               int32_t q;
               if constexpr (EPI == EPI_REQ16 || EPI == EPI_REQ32) {
@@ -278,9 +280,11 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
       // EPI_SILU (weight rows stacked as [gate 32 | up 32] blocks), (d, d + 32) of one head for EPI_QKV
       const int nc = n0 + cw;
       const double2 k0 = g.coef[nc], k1 = g.coef[nc + 32];
+      const double c10 = 256.0 * k0.x, c11 = 256.0 * k1.x;
       auto value16 = [&](int tm, int tn, int e) -> int32_t {   // SAT16(RS(acc * m, sh)) of column nc + 32 tn
         if constexpr (AW == 2) {
-          return rne_i32(fmin(fmax(req2(acc[tm][tn][1][e], acc[tm][tn][0][e], tn ? k1 : k0), -32768.0), 32767.0));
+          return rne_i32(fmin(fmax(req2(acc[tm][tn][1][e], acc[tm][tn][0][e], tn ? c11 : c10, tn ? k1 : k0),
+                                   -32768.0), 32767.0));
         } else {
           const int n = nc + 32 * tn;
           return (int32_t)clamp_bits16(rs(acc64(tm, tn, e, g.wsum[n]) * g.mult[n], g.shift[n]));
@@ -302,7 +306,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
 #pragma unroll
           for (int e = 0; e < 16; ++e) { gv[e] = value16(tm, 0, e); uv[e] = value16(tm, 1, e); }
 #pragma unroll
-          for (int e = 0; e < 16; ++e) sv[e] = g.aux_tab[gv[e] + 32768];   // the table gathers together
+          for (int e = 0; e < 16; ++e) sv[e] = g.aux_tab[(uint32_t)(gv[e] + 32768)];   // the table gathers together
 #pragma unroll
           for (int e = 0; e < 16; ++e) {
             // SAT(RS(silu * up, sh2), bits2): the product and the scaled sum are exact in float64
@@ -310,12 +314,17 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
             const int32_t v = rne_i32(fmin(fmax(fma(x, sc, half), lo), hi));
             if (!live(tm, e)) continue;
             uint8_t* ob = tb + o0 + (uint32_t)(roff(e) * 64);
+            // limb bytes: the low bytes carry the -128 bias, the top byte is signed
             if (g.bits2 == 16) {
-              ob[0] = (uint8_t)limb_byte(v, 0, 2);
-              ob[pl] = (uint8_t)limb_byte(v, 1, 2);
+              const uint32_t vb = (uint32_t)v ^ 0x80u;
+              ob[0] = (uint8_t)vb;
+              ob[pl] = (uint8_t)(vb >> 8);
             } else {
-#pragma unroll
-              for (int l = 0; l < 4; ++l) ob[l * pl] = (uint8_t)limb_byte(v, l, 4);
+              const uint32_t vb = (uint32_t)v ^ 0x808080u;
+              ob[0] = (uint8_t)vb;
+              ob[pl] = (uint8_t)(vb >> 8);
+              ob[2 * pl] = (uint8_t)(vb >> 16);
+              ob[3 * pl] = (uint8_t)(vb >> 24);
             }
           }
         }

@@ -21,7 +21,17 @@ namespace eii {
 namespace {
 
 constexpr int kBK = 64;          // K block: one MFMA K-step
-constexpr int kLdsRow = 80;      // LDS bytes per 64-byte row: 16-lane b128 reads hit 64 distinct banks
+// LDS rows of the activation tile are 64 bytes (one K block); the 16-byte chunk c of row r sits at
+// chunk c ^ ((r >> 2) & 3), so both the direct-to-LDS loads (lane order) and the 16-lane groups of
+// the fragment reads (16 consecutive rows, one chunk) cover all 64 banks.
+constexpr int kLdsRow = 64;
+// 16 bytes per lane from global memory straight into LDS: lane i writes lds + 16 i (lds is the
+// wave's base address; every lane passes the same one).  Kept out of the kernel templates: the
+// host compilation pass of a kernel that names the builtin directly drops the kernel's launch stub.
+__device__ __forceinline__ void dma16(const void* src, void* lds) { __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 0); }
+__device__ __forceinline__ int lds_swz(int row, int c) { return c ^ ((row >> 2) & 3); }
+// s_waitcnt immediate: vector memory count <= n, the other counters not waited for (gfx9 encoding)
+constexpr int vmcnt_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
 
 // Limb planes of 4 int16 values packed in two dwords: (low bytes - 128, high bytes).
 __device__ __forceinline__ uint32_t lo_bytes16(uint32_t d0, uint32_t d1) {
@@ -86,8 +96,9 @@ struct GemmCfg {
   static constexpr int WM = BM / 2, WN = 64;             // 2 x 2 waves
   static constexpr int TM = WM / 32, TN = 2;             // 32x32 tiles per wave
   static constexpr int kPlane = BM * kLdsRow;
-  static constexpr int kStage = AW * kPlane;              // activation limb planes only
-  static constexpr int kAChunks = AW * BM * 4 / kThreads;   // 16-byte global loads per thread
+  static constexpr int kStage = AW * kPlane;              // activation limb planes only: 16 KB
+  static constexpr int kStages = 4;                       // loaded three steps ahead
+  static constexpr int kAChunks = AW * BM * 4 / kThreads;   // 16-byte direct-to-LDS loads per thread
   static_assert(kAChunks * kThreads == AW * BM * 4, "chunk split");
 };
 
@@ -108,7 +119,7 @@ template <int AW, int EPI, int NK>
 __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
   using C = GemmCfg<AW>;
   static_assert(NK >= 1, "at least one K block");
-  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * C::kStage];
+  __shared__ __attribute__((aligned(16))) uint8_t smem[C::kStages * C::kStage];
   const int nMB = (g.M + C::BM - 1) / C::BM, nNB = (g.N + C::BN - 1) / C::BN, nT = nMB * nNB;
   // this workgroup's tiles: v = v0, v0 + stride, ... < vend
   const int xcd = blockIdx.x & 7, per = (nT + 7) / 8, nwg_x = gridDim.x >> 3;
@@ -122,60 +133,70 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
   const int fc = lane & 31, fh = lane >> 5;
   const uint8_t* Ab = (const uint8_t*)g.A;
 
-  // Load cursor: tile and K block of the next step to load, with this thread's source pointers
-  // for that tile (advanced incrementally; divisions happen once per tile).  Rows past M and
-  // column blocks past N read row M - 1 / the last block; their results are never stored.
-  // Both operands are laid out so that each wave load instruction reads contiguous 1 KB runs:
-  // K-blocked activation planes (16 rows x 64 bytes) and fragment-ordered weights.
-  int l_tile = 0, l_kb = 0;
+  // Operand loads run ahead of the MFMAs on a fixed schedule: the activations of step s + LA go
+  // straight from global memory into LDS stage (s + LA) % 4 (lane i of a load lands at its base
+  // + 16 i, so each lane fetches the chunk that belongs at its slot), and the weight fragments of
+  // step s + LW into register set (s + LW) % 2.  LA <= NK and LW <= NK, so a load belongs to the
+  // current tile or the next one, and the source pointers switch to the next tile at the step
+  // that first loads from it.  Past the last tile the loads repeat the last tile (addresses stay
+  // valid, nothing reads them), so every step issues the same loads and the memory-count waits
+  // are the same everywhere.  Rows past M read row M - 1 and column blocks past N the last block;
+  // their results are never stored.  Both operands are laid out for contiguous 1 KB wave runs:
+  // K-blocked activation planes and fragment-ordered weights.
+  constexpr int LA = nk >= 3 ? 3 : nk, LW = nk >= 2 ? 2 : 1;
+  static_assert(LA >= LW && LA < C::kStages, "activations are loaded no later than the weights of a step");
   const size_t a_kstep = (size_t)g.M * 64;              // activation bytes between K blocks
   const int nb32_last = (g.N + 31) / 32 - 1;
   const uint8_t* a_src[C::kAChunks];
   const int8_t* w_src[C::TN];
-  auto set_load_tile = [&](int j) __attribute__((always_inline)) {
-    int mb, nb;
-    tile_coords(v0 + j * nwg_x, nMB, nNB, mb, nb);
-    const int m0 = mb * C::BM, n0 = nb * C::BN;
+  auto coords = [&](int j, int& mb, int& nb) __attribute__((always_inline)) {
+    tile_coords(v0 + min(j, ntiles - 1) * nwg_x, nMB, nNB, mb, nb);
+  };
+  auto point_a = [&](int mb) __attribute__((always_inline)) {
+    const int m0 = mb * C::BM;
 #pragma unroll
     for (int i = 0; i < C::kAChunks; ++i) {
-      // chunk q: limb plane l, row, 16-byte chunk c
-      const int q = tid + C::kThreads * i, l = q / (4 * C::BM), row = (q >> 2) % C::BM, c = q & 3;
+      // LDS slot q (16 bytes) of the stage: limb plane l, row, physical chunk cp
+      const int q = tid + C::kThreads * i, l = q / (4 * C::BM), row = (q >> 2) % C::BM, cp = q & 3;
       const int m = min(m0 + row, g.M - 1);
-      a_src[i] = Ab + (size_t)l * g.a_plane + (size_t)m * 64 + c * 16;
+      a_src[i] = Ab + (size_t)l * g.a_plane + (size_t)m * 64 + lds_swz(row, cp) * 16;
     }
+  };
+  auto point_w = [&](int nb) __attribute__((always_inline)) {
 #pragma unroll
     for (int tn = 0; tn < C::TN; ++tn) {
       // this lane's B fragments: weight rows n0 + 64 wn + 32 tn + 0..31, the lane's 16 bytes of
       // each 32-column K slice
-      const int nb32 = min((n0 + wn * C::WN + 32 * tn) >> 5, nb32_last);
+      const int nb32 = min((nb * C::BN + wn * C::WN + 32 * tn) >> 5, nb32_last);
       w_src[tn] = g.W + (size_t)nb32 * (g.K / 32) * 1024 + lane * 16;
     }
   };
-  u32x4 areg[2][C::kAChunks];
-  v4i wreg[2][C::TN][2];
-  auto load = [&](auto SET) __attribute__((always_inline)) {   // the step at the cursor, into register set SET (compile time)
-    constexpr int set = decltype(SET)::value;
-    const size_t ka = (size_t)l_kb * a_kstep;
-    const int kw = l_kb * 2048;
+  // The pointers advance by one K block per load.  The increment goes through an empty asm so
+  // that the compiler keeps one pointer set per operand instead of precomputing the addresses of
+  // every step of the unrolled tile.
+  auto opaque = [](size_t v) __attribute__((always_inline)) {
+    __asm__ volatile("" : "+s"(v));
+    return v;
+  };
+  auto load_a = [&](int st) __attribute__((always_inline)) {   // next K block -> stage st % 4
+    uint8_t* stage = smem + (st & (C::kStages - 1)) * C::kStage;
 #pragma unroll
-    for (int i = 0; i < C::kAChunks; ++i) areg[set][i] = *(const u32x4*)(a_src[i] + ka);
+    for (int i = 0; i < C::kAChunks; ++i)
+      dma16(a_src[i], stage + (C::kThreads * i + 64 * wave) * 16);
+    const size_t inc = opaque(a_kstep);
+#pragma unroll
+    for (int i = 0; i < C::kAChunks; ++i) a_src[i] += inc;
+  };
+  v4i wreg[2][C::TN][2];
+  auto load_w = [&](auto SET) __attribute__((always_inline)) {   // next K block -> register set SET
+    constexpr int set = decltype(SET)::value;
 #pragma unroll
     for (int tn = 0; tn < C::TN; ++tn)
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) wreg[set][tn][ks] = *(const v4i*)(w_src[tn] + kw + 1024 * ks);
-    if (++l_kb == nk) {
-      l_kb = 0;
-      if (++l_tile < ntiles) set_load_tile(l_tile);
-    }
-  };
-  auto store = [&](auto SET) __attribute__((always_inline)) {   // activation register set SET into LDS stage SET
-    constexpr int set = decltype(SET)::value;
-    uint8_t* base = smem + set * C::kStage;
+      for (int ks = 0; ks < 2; ++ks) wreg[set][tn][ks] = *(const v4i*)(w_src[tn] + 1024 * ks);
+    const size_t inc = opaque(2048);
 #pragma unroll
-    for (int i = 0; i < C::kAChunks; ++i) {
-      const int q = tid + C::kThreads * i, l = q / (4 * C::BM), row = (q >> 2) % C::BM, c = q & 3;
-      *(u32x4*)(base + l * C::kPlane + row * kLdsRow + c * 16) = areg[set][i];
-    }
+    for (int tn = 0; tn < C::TN; ++tn) w_src[tn] += inc;
   };
 
   v16i acc[C::TM][C::TN][AW];
@@ -396,32 +417,48 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
     }
   };
 
-  // Step s computes from LDS stage s % 2 and weight register set s % 2; both were loaded two
-  // steps earlier, the activations stored to LDS during step s - 1.  Every tile is unrolled
-  // (two tiles per iteration when NK is odd), so the parity of each step is a compile-time
-  // constant and the code between waits is straight-line.
+  // Step s computes from LDS stage s % 4 and weight register set s % 2.  It waits for its own
+  // loads with an explicit memory-count wait before the barrier, so the barrier carries no full
+  // memory fence and the later loads stay in flight: with LW = 2, the loads issued after the
+  // weights of step s are the activations of s + LA - 1 and the weights of s + 1 (the prologue
+  // issues in the same order), and loads complete in order.  Every tile is unrolled (two tiles per
+  // iteration when NK is odd), so the register set of each step is a compile-time constant and a
+  // tile is straight-line code up to its epilogue.
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
-  const int nsteps = ntiles * nk;
-  set_load_tile(0);
-  load(I0{});
-  if (nsteps > 1) load(I1{});
-  store(I0{});
-  __syncthreads();
-  // step kb of tile jt (cur = parity of the global step); more = a step two ahead exists
-  auto step = [&](auto CUR, int jt, int kb, bool more2, bool more1) __attribute__((always_inline)) {
+  constexpr int kAfterW = LW == 2 ? C::kAChunks + 2 * C::TN : 0;
+  int mb, nb, mb_next, nb_next;
+  coords(0, mb, nb);
+  point_a(mb);
+  point_w(nb);
+#pragma unroll
+  for (int i = 0; i + 1 < LA; ++i) load_a(i);
+  if constexpr (LW == 2) load_w(I0{});
+  load_a(LA - 1);
+  if constexpr (LW == 2) load_w(I1{});
+  else load_w(I0{});
+  // step kb of tile jt: global step st = jt * nk + kb, cur = st % 2
+  auto step = [&](auto CUR, int jt, int kb, int st) __attribute__((always_inline)) {
     constexpr int cur = decltype(CUR)::value;
-    using NXT = std::integral_constant<int, cur ^ 1>;
-    const uint8_t* base = smem + cur * C::kStage;
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(kAfterW));
+    __builtin_amdgcn_s_barrier();
+    __asm__ volatile("" ::: "memory");
+    if (kb == 0) coords(jt + 1, mb_next, nb_next);
+    // activations of st + LA, into the stage every wave finished reading last step
+    if (kb + LA == nk) point_a(mb_next);
+    load_a(st + LA);
+    const uint8_t* base = smem + (st & (C::kStages - 1)) * C::kStage;
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      const int fk = 32 * ks + 16 * fh;
+      const int kc = 2 * ks + fh;   // this lane's 16-byte K chunk
       v4i af[C::TM][AW];   // all A fragments of this K step first, so their LDS latencies overlap
 #pragma unroll
       for (int tm = 0; tm < C::TM; ++tm)
 #pragma unroll
-        for (int l = 0; l < AW; ++l)
-          af[tm][l] = *(const v4i*)(base + l * C::kPlane + (wm * C::WM + tm * 32 + fc) * kLdsRow + fk);
+        for (int l = 0; l < AW; ++l) {
+          const int row = wm * C::WM + tm * 32 + fc;
+          af[tm][l] = *(const v4i*)(base + l * C::kPlane + row * kLdsRow + lds_swz(row, kc) * 16);
+        }
 #pragma unroll
       for (int tm = 0; tm < C::TM; ++tm)
 #pragma unroll
@@ -429,16 +466,15 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
 #pragma unroll
           for (int tn = 0; tn < C::TN; ++tn) acc[tm][tn][l] = mfma32(af[tm][l], wreg[cur][tn][ks], acc[tm][tn][l]);
     }
-    // the weight registers of this step are consumed: the prefetch two steps ahead reuses them
-    if (more2) load(CUR);
-    if (more1) store(NXT{});
-    __syncthreads();
+    // weights of st + LW, into the set this step just consumed (LW = 2) or the other one
+    if (kb + LW == nk) point_w(nb_next);
+    load_w(std::integral_constant<int, (cur + LW) % 2>{});
     if (kb != nk - 1) return;
 
     // ---------------------------------------------------------------- epilogue
-    int mb, nb;
-    tile_coords(v0 + jt * nwg_x, nMB, nNB, mb, nb);
     epilogue(mb, nb);
+    mb = mb_next;
+    nb = nb_next;
 #pragma unroll
     for (int a = 0; a < C::TM; ++a)
 #pragma unroll
@@ -451,9 +487,8 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
 #pragma unroll
     for (int kb = 0; kb < nk; ++kb) {
       const int st = jt * nk + kb;
-      const bool more1 = st + 1 < nsteps, more2 = st + 2 < nsteps;
-      if ((kb + p0) % 2 == 0) step(I0{}, jt, kb, more2, more1);
-      else step(I1{}, jt, kb, more2, more1);
+      if ((kb + p0) % 2 == 0) step(I0{}, jt, kb, st);
+      else step(I1{}, jt, kb, st);
     }
   };
   if constexpr (nk % 2 == 0) {
@@ -466,6 +501,8 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
     }
     if (jt < ntiles) tile(I0{}, jt);
   }
+  // the loads issued past the last tile write this workgroup's LDS: drain them before it ends
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 }
 
 int device_cus() {

@@ -208,14 +208,18 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
       for (int l = 0; l < AW; ++l) acc[a][b][l] = v16i{};
 
   // Epilogue of tile (mb, nb).  Lane value (tm, tn, e) sits at tile row rw + 32 tm + roff(e)
-  // (rw = wm WM + 4 fh) and tile column cw + 32 tn (cw = wn WN + fc).  Addresses are 32-bit
-  // offsets from per-tile bases; loads are unconditional (rows past M read row M - 1) so they
-  // issue back to back, and only the stores test the row.
-  auto epilogue = [&](int mb, int nb) __attribute__((always_inline)) {
+  // (rw = wm WM + 4 fh) and tile column cw + 32 tn (cw = wn WN + fc): the 32 lanes of a half-wave
+  // cover 32 consecutive columns of one row, so every load and store moves whole 128-byte lines.
+  // Tiles inside M (all but the last row block) take a path without row tests, where every
+  // address is a uniform row base (scalar registers, scalar arithmetic) plus the lane's fixed
+  // 32-bit offset, so element addresses cost no vector instructions.  The last row block clamps
+  // its loads to row M - 1 and tests the row at each store.
+  auto epilogue_t = [&](auto FULL, int mb, int nb) __attribute__((always_inline)) {
+    constexpr bool full = decltype(FULL)::value;
     const int m0 = mb * C::BM, n0 = nb * C::BN;
     const int rw = wm * C::WM + 4 * fh, cw = wn * C::WN + fc;
     auto roff = [](int e) { return 8 * (e >> 2) + (e & 3); };
-    auto live = [&](int tm, int e) { return m0 + rw + 32 * tm + roff(e) < g.M; };
+    auto live = [&](int tm, int e) { return full || m0 + rw + 32 * tm + roff(e) < g.M; };
     const int rlast = g.M - 1 - m0;   // last valid tile row
     // the row stride passes through an empty asm so the per-element offsets are recomputed here
     // instead of being hoisted out of the tile loop (64 loop-invariant offsets would spill)
@@ -228,12 +232,28 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
       for (int l = 0; l < AW; ++l) a += (int64_t)acc[tm][tn][l][e] * ((int64_t)1 << (8 * l));
       return a;
     };
+    // Element (tm, e, column offset col) of a row-major tile with rows of ld elements at `tile`:
+    // the uniform part (tile, row 32 tm + roff(e), col) and the lane part (row rw, column cw) are
+    // added separately.  rowL clamps the row for loads in the last row block.
+    auto at = [&](auto* tile, int ld, uint32_t lane_b, int tm, int e, int col) {
+      using T = std::remove_pointer_t<decltype(tile)>;
+      return (T*)((char*)(tile + (size_t)(32 * tm + roff(e)) * ld + col) + lane_b);
+    };
+    auto atL = [&](auto* tile, int ld, uint32_t lane_b, int tm, int e, int col) {
+      using T = std::remove_pointer_t<decltype(tile)>;
+      if constexpr (full) return at(tile, ld, lane_b, tm, e, col);
+      else return tile + (size_t)min(rw + 32 * tm + roff(e), rlast) * ld + cw + col;
+    };
 
     if constexpr (EPI == EPI_I64 || EPI == EPI_REQ16 || EPI == EPI_REQ32 || EPI == EPI_RESID || EPI == EPI_LOGITS) {
       using OT = std::conditional_t<EPI == EPI_I64, int64_t, std::conditional_t<EPI == EPI_REQ16, int16_t, int32_t>>;
-      OT* tb = (OT*)g.out + (size_t)m0 * g.N + n0;
+      OT* tb = (OT*)g.out + (size_t)m0 * N + n0;
+      const uint32_t lane_b = ((uint32_t)rw * (uint32_t)N + (uint32_t)cw) * (uint32_t)sizeof(OT);
       const double lo = EPI == EPI_REQ16 || EPI == EPI_REQ32 ? -ldexp(1.0, g.sat_bits - 1) : 0.0;
       const double hi = EPI == EPI_REQ16 || EPI == EPI_REQ32 ? ldexp(1.0, g.sat_bits - 1) - 1.0 : 0.0;
+      // logits leave int32 iff RNE(y) does: y is never a tie, so iff y > 2^31 - 1/2 or y < -2^31 - 1/2
+      double ymax = 0.0, ymin = 0.0;
+      bool bad = false;
 #pragma unroll
       for (int tn = 0; tn < C::TN; ++tn) {
         const int n = n0 + cw + 32 * tn;
@@ -244,15 +264,12 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
         if constexpr (AW == 4 && EPI != EPI_I64) { mu = g.mult[n]; sh = g.shift[n]; }
         if constexpr (AW == 2 && EPI != EPI_I64) k = g.coef[n];
         const double c1 = 256.0 * k.x;
-        bool bad = false;
 #pragma unroll
         for (int tm = 0; tm < C::TM; ++tm) {
-          const uint32_t o0 = (uint32_t)(rw + 32 * tm) * (uint32_t)N + (uint32_t)(cw + 32 * tn);
-          auto at = [&](int e) { return o0 + (uint32_t)(roff(e) * N); };
           if constexpr (EPI == EPI_I64) {
 #pragma unroll
             for (int e = 0; e < 16; ++e)
-              if (live(tm, e)) tb[at(e)] = acc64(tm, tn, e, ws);
+              if (live(tm, e)) *at(tb, N, lane_b, tm, e, 32 * tn) = acc64(tm, tn, e, ws);
             continue;
           }
           // residual epilogue: the loads of 8 rows issue together, then their updates
@@ -261,13 +278,12 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
             int32_t xv[8];
             if constexpr (EPI == EPI_RESID) {
 #pragma unroll
-              for (int i = 0; i < 8; ++i)
-                xv[i] = tb[(uint32_t)min(rw + 32 * tm + roff(eh + i), rlast) * (uint32_t)N + (uint32_t)(cw + 32 * tn)];
+              for (int i = 0; i < 8; ++i) xv[i] = *atL(tb, N, lane_b, tm, eh + i, 32 * tn);
             }
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
               const int e = eh + i;
-              // RS(acc * m, sh): exact integer-valued double + 2^-(sh+1) offset (2 limbs) or int64 (4 limbs)
+              // RS(acc * m, sh): exact float64 2^-(sh+1)-offset form (2 limbs) or int64 (4 limbs)
               double y = 0.0;
               int64_t v = 0;
               if constexpr (AW == 2) y = req2(acc[tm][tn][1][e], acc[tm][tn][0][e], c1, k);
@@ -280,21 +296,21 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
                             : (int32_t)clamp_bits32((int64_t)xv[i] + v);
               } else {   // EPI_LOGITS
                 if constexpr (AW == 2) {
-                  const double t2 = rint(y);
-                  bad |= t2 > 2147483647.0 || t2 < -2147483648.0;
-                  q = rne_i32(t2);
+                  ymax = fmax(ymax, y);
+                  ymin = fmin(ymin, y);
+                  q = rne_i32(y);
                 } else {
                   bad |= v != (int64_t)(int32_t)v;
                   q = (int32_t)v;
                 }
               }
-              if (live(tm, e)) tb[at(e)] = (OT)q;
+              if (live(tm, e)) *at(tb, N, lane_b, tm, e, 32 * tn) = (OT)q;
             }
           }
         }
-        if constexpr (EPI == EPI_LOGITS) {
-          if (bad) atomicOr(g.flag, 1);
-        }
+      }
+      if constexpr (EPI == EPI_LOGITS) {
+        if (bad || ymax > 2147483647.5 || ymin < -2147483648.5) atomicOr(g.flag, 1);
       }
     } else if (n0 + wn * C::WN < g.N) {
       // columns c (tn = 0) and 32 + c (tn = 1) of the wave's 64-column block: (gate j, up j) for
@@ -302,39 +318,46 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
       const int nc = n0 + cw;
       const double2 k0 = g.coef[nc], k1 = g.coef[nc + 32];
       const double c10 = 256.0 * k0.x, c11 = 256.0 * k1.x;
-      auto value16 = [&](int tm, int tn, int e) -> int32_t {   // SAT16(RS(acc * m, sh)) of column nc + 32 tn
+      auto scaled = [&](int tm, int tn, int e) -> double {   // RS(acc * m, sh) of column nc + 32 tn, 2 limbs
+        return req2(acc[tm][tn][1][e], acc[tm][tn][0][e], tn ? c11 : c10, tn ? k1 : k0);
+      };
+      auto value16 = [&](int tm, int tn, int e) -> int32_t {   // SAT16(RS(acc * m, sh))
         if constexpr (AW == 2) {
-          return rne_i32(fmin(fmax(req2(acc[tm][tn][1][e], acc[tm][tn][0][e], tn ? c11 : c10, tn ? k1 : k0),
-                                   -32768.0), 32767.0));
+          return rne_i32(fmin(fmax(scaled(tm, tn, e), -32768.0), 32767.0));
         } else {
           const int n = nc + 32 * tn;
           return (int32_t)clamp_bits16(rs(acc64(tm, tn, e, g.wsum[n]) * g.mult[n], g.shift[n]));
         }
       };
+      auto value16d = [&](int tm, int tn, int e) -> double {   // the same as a double
+        if constexpr (AW == 2) return rint(fmin(fmax(scaled(tm, tn, e), -32768.0), 32767.0));
+        else return (double)value16(tm, tn, e);
+      };
       if constexpr (EPI == EPI_SILU) {
         // gated limb planes (bits2 / 8 planes of M x N / 2, K-blocked): the lane's gated column
         // n0 / 2 + wn 32 + fc lies in 64-column block nb at offset wn 32 + fc
-        const int NG = N / 2;
         const double lo = -ldexp(1.0, g.bits2 - 1), hi = ldexp(1.0, g.bits2 - 1) - 1.0;
         // RS(x, sh) = RNE(x 2^-sh + 2^-(sh+1)) for sh >= 1; for sh <= 0 the scaled value is an integer
         const double sc = ldexp(1.0, -g.sh2), half = g.sh2 >= 1 ? ldexp(0.5, -g.sh2) : 0.0;
-        const size_t pl = (size_t)g.M * NG;
+        const size_t pl = (size_t)g.M * (N / 2);
         uint8_t* tb = (uint8_t*)g.out + (size_t)nb * g.M * 64 + (size_t)m0 * 64;
+        const uint32_t lane_b = (uint32_t)rw * 64u + (uint32_t)(wn * 32 + fc);
 #pragma unroll
         for (int tm = 0; tm < C::TM; ++tm) {
-          const uint32_t o0 = (uint32_t)(rw + 32 * tm) * 64u + (uint32_t)(wn * 32 + fc);
-          int32_t gv[16], uv[16], sv[16];
+          int32_t gv[16], sv[16];
+          double uv[16];
 #pragma unroll
-          for (int e = 0; e < 16; ++e) { gv[e] = value16(tm, 0, e); uv[e] = value16(tm, 1, e); }
+          for (int e = 0; e < 16; ++e) { gv[e] = value16(tm, 0, e); uv[e] = value16d(tm, 1, e); }
 #pragma unroll
-          for (int e = 0; e < 16; ++e) sv[e] = g.aux_tab[(uint32_t)(gv[e] + 32768)];   // the table gathers together
+          for (int e = 0; e < 16; ++e)   // the table gathers together; 32-bit offsets from the table base
+            sv[e] = *(const int32_t*)((const char*)g.aux_tab + (uint32_t)(gv[e] + 32768) * 4u);
 #pragma unroll
           for (int e = 0; e < 16; ++e) {
             // SAT(RS(silu * up, sh2), bits2): the product and the scaled sum are exact in float64
-            const double x = (double)sv[e] * (double)uv[e];
+            const double x = (double)sv[e] * uv[e];
             const int32_t v = rne_i32(fmin(fmax(fma(x, sc, half), lo), hi));
             if (!live(tm, e)) continue;
-            uint8_t* ob = tb + o0 + (uint32_t)(roff(e) * 64);
+            uint8_t* ob = at(tb, 64, lane_b, tm, e, 0);
             // limb bytes: the low bytes carry the -128 bias, the top byte is signed
             if (g.bits2 == 16) {
               const uint32_t vb = (uint32_t)v ^ 0x80u;
@@ -351,14 +374,14 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
         }
       } else {   // EPI_QKV: heads 0..8 q and 9..11 k get RoPE, 12..14 v are stored as they are
         const int head = (n0 + wn * C::WN) >> 6;
-        int16_t* tb = (int16_t*)g.out + (size_t)m0 * g.N + n0;
+        int16_t* tb = (int16_t*)g.out + (size_t)m0 * N + n0;
+        const uint32_t lane_b = ((uint32_t)rw * (uint32_t)N + (uint32_t)cw) * 2u;
         if (head >= 12) {
           // v: int16 rows and, when requested, the V^T limb planes (4 consecutive rows per dword;
           // rows up to the tile end fit vt_stride, so no row test there)
           const size_t vcol = (size_t)((head - 12) * 64 + fc) * g.vt_stride, vpl = (size_t)192 * g.vt_stride;
 #pragma unroll
           for (int tm = 0; tm < C::TM; ++tm) {
-            const uint32_t o0 = (uint32_t)(rw + 32 * tm) * (uint32_t)N + (uint32_t)cw;
 #pragma unroll
             for (int b = 0; b < 4; ++b) {
               int32_t v1[4], v2[4];
@@ -368,7 +391,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
                 v1[r] = value16(tm, 0, e);
                 v2[r] = value16(tm, 1, e);
                 if (live(tm, e)) {
-                  int16_t* op = tb + o0 + (uint32_t)(roff(e) * N);
+                  int16_t* op = at(tb, N, lane_b, tm, e, 0);
                   op[0] = (int16_t)v1[r];
                   op[32] = (int16_t)v2[r];
                 }
@@ -388,33 +411,38 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
           const double sc = ldexp(1.0, -shr), half = shr >= 1 ? ldexp(0.5, -shr) : 0.0;
 #pragma unroll
           for (int tm = 0; tm < C::TM; ++tm) {
-            const uint32_t o0 = (uint32_t)(rw + 32 * tm) * (uint32_t)N + (uint32_t)cw;
 #pragma unroll
             for (int b = 0; b < 4; ++b) {
               int32_t cs[4], sn[4];
 #pragma unroll
               for (int r = 0; r < 4; ++r) {
                 const int ps = g.pos[min(m0 + rw + 32 * tm + 8 * b + r, g.M - 1)];
-                cs[r] = g.cosT[ps * 32 + fc];
-                sn[r] = g.sinT[ps * 32 + fc];
+                const uint32_t o = (uint32_t)ps * 128u + (uint32_t)fc * 4u;   // byte offset of [ps][fc]
+                cs[r] = *(const int32_t*)((const char*)g.cosT + o);
+                sn[r] = *(const int32_t*)((const char*)g.sinT + o);
               }
 #pragma unroll
               for (int r = 0; r < 4; ++r) {
-              const int e = 4 * b + r;
-              const double a1 = (double)value16(tm, 0, e), a2 = (double)value16(tm, 1, e);
-              const double c = (double)cs[r], s2 = (double)sn[r];
-              const int32_t o1 = rne_i32(fmin(fmax(fma(fma(a1, c, -a2 * s2), sc, half), -32768.0), 32767.0));
-              const int32_t o2 = rne_i32(fmin(fmax(fma(fma(a2, c, a1 * s2), sc, half), -32768.0), 32767.0));
-              if (!live(tm, e)) continue;
-              int16_t* op = tb + o0 + (uint32_t)(roff(e) * N);
-              op[0] = (int16_t)o1;
-              op[32] = (int16_t)o2;
+                const int e = 4 * b + r;
+                const double a1 = value16d(tm, 0, e), a2 = value16d(tm, 1, e);
+                const double c = (double)cs[r], s2 = (double)sn[r];
+                const int32_t o1 = rne_i32(fmin(fmax(fma(fma(a1, c, -a2 * s2), sc, half), -32768.0), 32767.0));
+                const int32_t o2 = rne_i32(fmin(fmax(fma(fma(a2, c, a1 * s2), sc, half), -32768.0), 32767.0));
+                if (!live(tm, e)) continue;
+                int16_t* op = at(tb, N, lane_b, tm, e, 0);
+                op[0] = (int16_t)o1;
+                op[32] = (int16_t)o2;
               }
             }
           }
         }
       }
     }
+  };
+  auto epilogue = [&](int mb, int nb) __attribute__((always_inline)) {
+    // (the QKV epilogue keeps one copy: two of them exhaust the registers)
+    if (EPI != EPI_QKV && (mb + 1) * C::BM <= g.M) epilogue_t(std::true_type{}, mb, nb);
+    else epilogue_t(std::false_type{}, mb, nb);
   };
 
   // Step s computes from LDS stage s % 4 and weight register set s % 2.  It waits for its own

@@ -97,7 +97,7 @@ struct GemmCfg {
   static constexpr int TM = WM / 32, TN = 2;             // 32x32 tiles per wave
   static constexpr int kPlane = BM * kLdsRow;
   static constexpr int kStage = AW * kPlane;              // activation limb planes only: 16 KB
-  static constexpr int kStages = 4;                       // loaded three steps ahead
+  static constexpr int kStages = 4;                       // loaded two and three steps ahead
   static constexpr int kAChunks = AW * BM * 4 / kThreads;   // 16-byte direct-to-LDS loads per thread
   static_assert(kAChunks * kThreads == AW * BM * 4, "chunk split");
 };
@@ -133,18 +133,18 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
   const int fc = lane & 31, fh = lane >> 5;
   const uint8_t* Ab = (const uint8_t*)g.A;
 
-  // Operand loads run ahead of the MFMAs on a fixed schedule: the activations of step s + LA go
-  // straight from global memory into LDS stage (s + LA) % 4 (lane i of a load lands at its base
-  // + 16 i, so each lane fetches the chunk that belongs at its slot), and the weight fragments of
-  // step s + LW into register set (s + LW) % 2.  LA <= NK and LW <= NK, so a load belongs to the
-  // current tile or the next one, and the source pointers switch to the next tile at the step
-  // that first loads from it.  Past the last tile the loads repeat the last tile (addresses stay
-  // valid, nothing reads them), so every step issues the same loads and the memory-count waits
-  // are the same everywhere.  Rows past M read row M - 1 and column blocks past N the last block;
-  // their results are never stored.  Both operands are laid out for contiguous 1 KB wave runs:
-  // K-blocked activation planes and fragment-ordered weights.
-  constexpr int LA = nk >= 3 ? 3 : nk, LW = nk >= 2 ? 2 : 1;
-  static_assert(LA >= LW && LA < C::kStages, "activations are loaded no later than the weights of a step");
+  // Operand loads run ahead of the MFMAs on a fixed schedule, with steps in pairs (s, s + 1),
+  // s even.  At the start of a pair, after the pair's one barrier, the activations of steps s + 2
+  // and s + 3 go straight from global memory into LDS stages (s + 2) % 4 and (s + 3) % 4, which
+  // were last read in steps s - 2 and s - 1 (lane i of a load lands at its base + 16 i, so each
+  // lane fetches the chunk that belongs at its slot).  After its MFMAs, step s (s + 1) loads the
+  // weight fragments of step s + 2 (s + 3) into the register set it just consumed.  A load of K
+  // block 0 points the source pointers at its tile, later blocks advance them.  Past the last
+  // tile the loads repeat the last tile (addresses stay valid, nothing reads them), so every
+  // step issues the same loads and the memory-count waits are the same everywhere.  Rows past M
+  // read row M - 1 and column blocks past N the last block; their results are never stored.
+  // Both operands are laid out for contiguous 1 KB wave runs: K-blocked activation planes and
+  // fragment-ordered weights.
   const size_t a_kstep = (size_t)g.M * 64;              // activation bytes between K blocks
   const int nb32_last = (g.N + 31) / 32 - 1;
   const uint8_t* a_src[C::kAChunks];
@@ -197,6 +197,24 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
     const size_t inc = opaque(2048);
 #pragma unroll
     for (int tn = 0; tn < C::TN; ++tn) w_src[tn] += inc;
+  };
+
+  // the loads of step st (tile j, K block blk): block 0 re-points the pointers at tile j
+  auto a_step = [&](int j, int blk, int st) __attribute__((always_inline)) {
+    if (blk == 0) {
+      int mb_, nb_;
+      coords(j, mb_, nb_);
+      point_a(mb_);
+    }
+    load_a(st);
+  };
+  auto w_step = [&](auto SET, int j, int blk) __attribute__((always_inline)) {
+    if (blk == 0) {
+      int mb_, nb_;
+      coords(j, mb_, nb_);
+      point_w(nb_);
+    }
+    load_w(SET);
   };
 
   v16i acc[C::TM][C::TN][AW];
@@ -445,36 +463,31 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
     else epilogue_t(std::false_type{}, mb, nb);
   };
 
-  // Step s computes from LDS stage s % 4 and weight register set s % 2.  It waits for its own
-  // loads with an explicit memory-count wait before the barrier, so the barrier carries no full
-  // memory fence and the later loads stay in flight: with LW = 2, the loads issued after the
-  // weights of step s are the activations of s + LA - 1 and the weights of s + 1 (the prologue
-  // issues in the same order), and loads complete in order.  Every tile is unrolled (two tiles per
-  // iteration when NK is odd), so the register set of each step is a compile-time constant and a
-  // tile is straight-line code up to its epilogue.
+  // Step s computes from LDS stage s % 4 and weight register set s % 2.  Its loads are waited for
+  // with explicit memory counts (loads complete in order): at a pair start, all but the weights
+  // of step s + 1 (2 TN loads), followed by the barrier (which then carries no full memory fence,
+  // so the later loads stay in flight); mid-pair, all but the activations of s + 1, s + 2 and the
+  // weights of s + 1 issued since.  Every tile is unrolled (two tiles per iteration when NK is
+  // odd), so the register set of each step is a compile-time constant and a tile is straight-line
+  // code up to its epilogue.
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
-  constexpr int kAfterW = LW == 2 ? C::kAChunks + 2 * C::TN : 0;
-  int mb, nb, mb_next, nb_next;
-  coords(0, mb, nb);
-  point_a(mb);
-  point_w(nb);
-#pragma unroll
-  for (int i = 0; i + 1 < LA; ++i) load_a(i);
-  if constexpr (LW == 2) load_w(I0{});
-  load_a(LA - 1);
-  if constexpr (LW == 2) load_w(I1{});
-  else load_w(I0{});
+  a_step(0, 0, 0);
+  a_step(1 / nk, 1 % nk, 1);
+  w_step(I0{}, 0, 0);
+  w_step(I1{}, 1 / nk, 1 % nk);
   // step kb of tile jt: global step st = jt * nk + kb, cur = st % 2
   auto step = [&](auto CUR, int jt, int kb, int st) __attribute__((always_inline)) {
     constexpr int cur = decltype(CUR)::value;
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(kAfterW));
-    __builtin_amdgcn_s_barrier();
-    __asm__ volatile("" ::: "memory");
-    if (kb == 0) coords(jt + 1, mb_next, nb_next);
-    // activations of st + LA, into the stage every wave finished reading last step
-    if (kb + LA == nk) point_a(mb_next);
-    load_a(st + LA);
+    if constexpr (cur == 0) {
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * C::TN));
+      __builtin_amdgcn_s_barrier();
+      __asm__ volatile("" ::: "memory");
+      a_step(jt + (kb + 2) / nk, (kb + 2) % nk, st + 2);
+      a_step(jt + (kb + 3) / nk, (kb + 3) % nk, st + 3);
+    } else {
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * C::kAChunks + 2 * C::TN));
+    }
     const uint8_t* base = smem + (st & (C::kStages - 1)) * C::kStage;
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
@@ -494,15 +507,20 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
 #pragma unroll
           for (int tn = 0; tn < C::TN; ++tn) acc[tm][tn][l] = mfma32(af[tm][l], wreg[cur][tn][ks], acc[tm][tn][l]);
     }
-    // weights of st + LW, into the set this step just consumed (LW = 2) or the other one
-    if (kb + LW == nk) point_w(nb_next);
-    load_w(std::integral_constant<int, (cur + LW) % 2>{});
+    // order: the first K slice's fragment reads, two MFMAs, the second slice's reads (their
+    // latency hides behind the first slice's MFMAs), then the remaining MFMAs
+    __builtin_amdgcn_sched_group_barrier(0x100, C::TM * AW, 0);   // LDS reads
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);            // MFMA
+    __builtin_amdgcn_sched_group_barrier(0x100, C::TM * AW, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 4 * C::TM * AW - 2, 0);
+    // weights of st + 2, into the set this step just consumed
+    w_step(CUR, jt + (kb + 2) / nk, (kb + 2) % nk);
     if (kb != nk - 1) return;
 
     // ---------------------------------------------------------------- epilogue
+    int mb, nb;
+    coords(jt, mb, nb);
     epilogue(mb, nb);
-    mb = mb_next;
-    nb = nb_next;
 #pragma unroll
     for (int a = 0; a < C::TM; ++a)
 #pragma unroll

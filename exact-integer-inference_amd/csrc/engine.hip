@@ -596,7 +596,7 @@ int run_block(eii_model* m, int l, int32_t* x, int M, int nseq, int max_T, const
     ProfScope ps(m, EII_K_GEMM_GU, s);
     if (!tr) {   // gate and up projections with the SiLU table and the gated product in the epilogue
       GemmArgs g = gemm_args(L.gu, h, M, m->gated, 16);
-      g.aux_tab = L.silu; g.sh2 = sh_s; g.bits2 = L.bits[GATED];
+      g.aux_tab = L.silu; g.sh2 = sh_s; g.bits2 = L.bits[GATED]; g.tab_bits = L.bits[SILU];
       HIPCHK(gemm(g, h2b, EPI_SILU, s));
     } else {
       HIPCHK(gemm(gemm_args(L.gu, h, M, m->gu, 16), h2b, EPI_REQ16, s));

@@ -48,9 +48,9 @@ struct GemmArgs {
   // 2-limb inputs, every epilogue except EPI_I64: per-column float64 coefficients [N]
   // (m 2^-sh, 128 wsum m 2^-sh + 2^-(sh+1)) from gemm_coef
   const double2* coef = nullptr;
-  // EPI_SILU
+  // EPI_SILU: SiLU table [65536] (index gate + 32768) whose entries fit tab_bits bits
   const int32_t* aux_tab = nullptr;
-  int sh2 = 0, bits2 = 16;
+  int sh2 = 0, bits2 = 16, tab_bits = 32;
   // EPI_QKV
   const int32_t* pos = nullptr;
   const int32_t* cosT = nullptr;

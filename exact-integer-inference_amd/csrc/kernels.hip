@@ -119,7 +119,10 @@ template <int AW, int EPI, int NK>
 __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
   using C = GemmCfg<AW>;
   static_assert(NK >= 1, "at least one K block");
-  __shared__ __attribute__((aligned(16))) uint8_t smem[C::kStages * C::kStage];
+  // EPI_SILU: entries 32768 - kTabHalf .. 32768 + kTabHalf - 1 of a 16-bit SiLU table as int16
+  // after the stages (the gate values cluster around 0, so most table reads hit LDS)
+  constexpr int kTabHalf = 4096, kTabBytes = EPI == EPI_SILU ? 4 * kTabHalf : 0;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[C::kStages * C::kStage + kTabBytes];
   const int nMB = (g.M + C::BM - 1) / C::BM, nNB = (g.N + C::BN - 1) / C::BN, nT = nMB * nNB;
   // this workgroup's tiles: v = v0, v0 + stride, ... < vend
   const int xcd = blockIdx.x & 7, per = (nT + 7) / 8, nwg_x = gridDim.x >> 3;
@@ -127,6 +130,15 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
   if (v0 >= vend) return;
   const int ntiles = (vend - v0 + nwg_x - 1) / nwg_x;
   constexpr int nk = NK;
+  int16_t* const tabw = (int16_t*)(smem + C::kStages * C::kStage);
+  int tab_half = 0;   // 0: no LDS window (32-bit table), every read goes to global memory
+  if constexpr (EPI == EPI_SILU) {
+    if (g.tab_bits == 16) {
+      tab_half = kTabHalf;
+      for (int i = threadIdx.x; i < 2 * kTabHalf; i += C::kThreads) tabw[i] = (int16_t)g.aux_tab[32768 - kTabHalf + i];
+    }
+    __syncthreads();
+  }
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
@@ -366,9 +378,20 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
           double uv[16];
 #pragma unroll
           for (int e = 0; e < 16; ++e) { gv[e] = value16(tm, 0, e); uv[e] = value16d(tm, 1, e); }
+          // SiLU table reads: gates within the LDS window read it there, the others global memory
+          // (32-bit offsets from the table base; lanes served by LDS point at one shared line)
+          bool inw[16];
 #pragma unroll
-          for (int e = 0; e < 16; ++e)   // the table gathers together; 32-bit offsets from the table base
-            sv[e] = *(const int32_t*)((const char*)g.aux_tab + (uint32_t)(gv[e] + 32768) * 4u);
+          for (int e = 0; e < 16; ++e) {
+            const int wi = gv[e] + tab_half;
+            inw[e] = (uint32_t)wi < (uint32_t)(2 * tab_half);
+            sv[e] = tabw[min(max(wi, 0), 2 * kTabHalf - 1)];
+          }
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int32_t t = *(const int32_t*)((const char*)g.aux_tab + (uint32_t)(inw[e] ? 32768 : gv[e] + 32768) * 4u);
+            if (!inw[e]) sv[e] = t;
+          }
 #pragma unroll
           for (int e = 0; e < 16; ++e) {
             // SAT(RS(silu * up, sh2), bits2): the product and the scaled sum are exact in float64

@@ -270,7 +270,6 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
       return (T*)((char*)(tile + (size_t)(32 * tm + roff(e)) * ld + col) + lane_b);
     };
     auto atL = [&](auto* tile, int ld, uint32_t lane_b, int tm, int e, int col) {
-      using T = std::remove_pointer_t<decltype(tile)>;
       if constexpr (full) return at(tile, ld, lane_b, tm, e, col);
       else return tile + (size_t)min(rw + 32 * tm + roff(e), rlast) * ld + cw + col;
     };
@@ -805,7 +804,7 @@ __device__ __forceinline__ int32_t sum16x8(u32x4 d) {   // sum of the 8 int16 va
 }
 
 template <int OB, int NKT>
-__global__ __launch_bounds__(192) void attn_kernel(AttnArgs a) {
+__global__ __launch_bounds__(192) __attribute__((amdgpu_waves_per_eu(2))) void attn_kernel(AttnArgs a) {
   __shared__ int32_t etab[kDMax + 2];                        // exp table, etab[1537] = 0
   __shared__ __attribute__((aligned(16))) int32_t skl[3][32];   // per wave: 128 * sum_d k per key
 
@@ -842,15 +841,25 @@ __global__ __launch_bounds__(192) void attn_kernel(AttnArgs a) {
     cq = 128 * sum - (1 << 20) + (1 << (sh - 1));   // with the rounding offset of RS(., sh)
   }
 
+  // K rows of key tile g for this lane (row pi(c) of the tile, d = 32 s + 16 h + 0..15), loaded
+  // one tile ahead of their use
+  struct KRows { u32x4 d[2][2]; };
+  auto load_k = [&](int g, KRows& kr) __attribute__((always_inline)) {
+    const int16_t* kp = a.qkv + (size_t)min(32 * g + pic, a.M - 1) * kQKVN + kD + kvg * 64 + 16 * h;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      kr.d[s][0] = *(const u32x4*)(kp + 32 * s);
+      kr.d[s][1] = *(const u32x4*)(kp + 32 * s + 8);
+    }
+  };
   // Scores SAT16(RS(q.k, sh)) of key tile g for this lane's query, keys 16 h + j.  The sum
   // acc + 2^(sh-1) = 65536 wv + lo16 with lo16 in [0, 65536) is evaluated in int32 pieces.
-  auto scores = [&](int g, int32_t (&sc)[16]) __attribute__((always_inline)) {
-    const int16_t* kp = a.qkv + (size_t)min(32 * g + pic, a.M - 1) * kQKVN + kD + kvg * 64 + 16 * h;
+  auto scores = [&](int g, const KRows& kr, int32_t (&sc)[16]) __attribute__((always_inline)) {
     v4i kl[2], kh[2];
     int32_t ks = 0;
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      const u32x4 d0 = *(const u32x4*)(kp + 32 * s), d1 = *(const u32x4*)(kp + 32 * s + 8);
+      const u32x4 d0 = kr.d[s][0], d1 = kr.d[s][1];
       kl[s] = v4i{(int)lo_bytes16(d0[0], d0[1]), (int)lo_bytes16(d0[2], d0[3]), (int)lo_bytes16(d1[0], d1[1]),
                   (int)lo_bytes16(d1[2], d1[3])};
       kh[s] = v4i{(int)hi_bytes16(d0[0], d0[1]), (int)hi_bytes16(d0[2], d0[3]), (int)hi_bytes16(d1[0], d1[1]),
@@ -871,19 +880,27 @@ __global__ __launch_bounds__(192) void attn_kernel(AttnArgs a) {
     const v4i* kk = (const v4i*)&skl[w][16 * h];
     const v4i k4[4] = {kk[0], kk[1], kk[2], kk[3]};
     __builtin_amdgcn_wave_barrier();
-    const bool edge = 32 * g < s0 || 32 * g + 31 > q0;
+    int32_t lo[16], wv[16];
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-      const int32_t lo = a8[j] * 256 + a0[j] + k4[j >> 2][j & 3] + cq;
-      const int32_t wv = a16[j] + (lo >> 16);
-      int32_t v = sh >= 16 ? wv >> (sh - 16)
-                           : min(max(wv, -32769), 32768) * (1 << (16 - sh)) + ((lo & 0xFFFF) >> sh);
-      v = min(max(v, -32768), 32767);
-      if (edge) {
+      lo[j] = a8[j] * 256 + a0[j] + k4[j >> 2][j & 3] + cq;
+      wv[j] = a16[j] + (lo[j] >> 16);
+    }
+    // the shift is uniform: one branch per tile
+    if (sh >= 16) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) sc[j] = min(max(wv[j] >> (sh - 16), -32768), 32767);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        sc[j] = min(max(min(max(wv[j], -32769), 32768) * (1 << (16 - sh)) + ((lo[j] & 0xFFFF) >> sh), -32768), 32767);
+    }
+    if (32 * g < s0 || 32 * g + 31 > q0) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
         const int key = 32 * g + 16 * h + j;
-        if (key < s0 || key > qi) v = kMasked;
+        if (key < s0 || key > qi) sc[j] = kMasked;
       }
-      sc[j] = v;
     }
   };
   // e = E[rowmax - s] for d <= 1536, else 0; masked keys 0
@@ -901,19 +918,31 @@ __global__ __launch_bounds__(192) void attn_kernel(AttnArgs a) {
   for (int i = 0; i < 2; ++i) C16[i] = C8[i] = C0[i] = v16i{};
   int32_t SP = 0;
   double Zd = 0.0, rZ = 0.0, Zh = 0.0;
-  // P = floor((e 65536 + floor(Z / 2)) / Z) (python/intref.py:245-246): the float64 quotient is
-  // within one of the truth and the exact float64 remainder corrects it
+  // P = floor((e 65536 + floor(Z / 2)) / Z) (python/intref.py:245-246).  num / Z <= 65536.5 (e is
+  // a term of Z), and num rZ + 2^-30 evaluated with one fma is within 2^-36 of num / Z + 2^-30, so
+  // its floor is the true quotient or one more; the exact float64 remainder takes the one back.
   auto prob = [&](int32_t e) __attribute__((always_inline)) -> int32_t {
     const double num = fma((double)e, 65536.0, Zh);
-    const double q = floor(num * rZ);
+    const double q = floor(fma(num, rZ, 0x1p-30));
     const double rem = fma(-q, Zd, num);
-    return (int32_t)q + (rem >= Zd ? 1 : 0) - (rem < 0.0 ? 1 : 0);
+    return (int32_t)q - (rem < 0.0 ? 1 : 0);
   };
   // probabilities of key tile g (e values) into limb operands, then the P.V MFMAs.  R1 =
   // (P + 128) >> 8 in [0, 256] goes in as P1 = min(R1, 127) plus, in the waves where some R1
   // exceeds 127 (a key holding about half the weight or more), P1b = min(R1 - P1, 127) and
   // P1c = R1 - P1 - P1b, all with the weight of P1.
-  auto pv = [&](int g, const int32_t (&ev)[16]) __attribute__((always_inline)) {
+  // V^T limb fragments of key tile g (A operands of the two 32-row d tiles), loaded one tile ahead
+  struct VFrag { v4i L[2], H[2]; };
+  auto load_v = [&](int g, VFrag& vf) __attribute__((always_inline)) {
+    const size_t vpl = (size_t)192 * vts;
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt) {
+      const uint8_t* vp = a.vt + (size_t)(kvg * 64 + 32 * dt + c) * vts + 32 * g + 16 * h;
+      vf.L[dt] = *(const v4i*)vp;
+      vf.H[dt] = *(const v4i*)(vp + vpl);
+    }
+  };
+  auto pv = [&](const VFrag& vf, const int32_t (&ev)[16]) __attribute__((always_inline)) {
     uint32_t w0[4], w1[4];
     int32_t rest[16];
     int32_t anyrest = 0;
@@ -934,14 +963,8 @@ __global__ __launch_bounds__(192) void attn_kernel(AttnArgs a) {
     }
     const v4i P0 = v4i{(int)w0[0], (int)w0[1], (int)w0[2], (int)w0[3]};
     const v4i P1 = v4i{(int)w1[0], (int)w1[1], (int)w1[2], (int)w1[3]};
-    const size_t vpl = (size_t)192 * vts;
-    v4i VL[2], VH[2];
-#pragma unroll
-    for (int dt = 0; dt < 2; ++dt) {
-      const uint8_t* vp = a.vt + (size_t)(kvg * 64 + 32 * dt + c) * vts + 32 * g + 16 * h;
-      VL[dt] = *(const v4i*)vp;
-      VH[dt] = *(const v4i*)(vp + vpl);
-    }
+    const v4i* VL = vf.L;
+    const v4i* VH = vf.H;
 #pragma unroll
     for (int dt = 0; dt < 2; ++dt) {
       C16[dt] = mfma32(VH[dt], P1, C16[dt]);
@@ -986,13 +1009,24 @@ __global__ __launch_bounds__(192) void attn_kernel(AttnArgs a) {
   };
 
   int32_t rowmax = kMasked;
+  // with up to 5 key tiles the registers hold K and V one tile ahead of their use as well
+  constexpr bool ahead = NKT > 0 && NKT <= 5;
+  KRows kr[ahead ? 2 : 1];
+  VFrag vf[ahead ? 2 : 1];
   if constexpr (NKT > 0) {
     uint32_t pk[NKT][8];   // packed int16 scores
+    if constexpr (ahead) load_k(g0, kr[0]);
 #pragma unroll
     for (int t = 0; t < NKT; ++t) {
       if (t < ntile) {
+        if constexpr (ahead) {
+          if (t + 1 < ntile) load_k(g0 + t + 1, kr[(t + 1) & 1]);
+          else load_v(g0, vf[0]);   // the first V tile, while the last scores and the sums run
+        } else {
+          load_k(g0 + t, kr[0]);
+        }
         int32_t sc[16];
-        scores(g0 + t, sc);
+        scores(g0 + t, kr[ahead ? t & 1 : 0], sc);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           pk[t][i] = ((uint32_t)sc[2 * i] & 0xFFFFu) | ((uint32_t)sc[2 * i + 1] << 16);
@@ -1016,16 +1050,22 @@ __global__ __launch_bounds__(192) void attn_kernel(AttnArgs a) {
 #pragma unroll
     for (int t = 0; t < NKT; ++t)
       if (t < ntile) {
+        if constexpr (ahead) {
+          if (t + 1 < ntile) load_v(g0 + t + 1, vf[(t + 1) & 1]);
+        } else {
+          load_v(g0 + t, vf[0]);
+        }
         int32_t ev[16];
 #pragma unroll
         for (int j = 0; j < 16; ++j) ev[j] = expo(g0 + t, j, unpack(t, j), rowmax);
-        pv(g0 + t, ev);
+        pv(vf[ahead ? t & 1 : 0], ev);
       }
   } else {
 #pragma unroll 1
     for (int t = 0; t < ntile; ++t) {
       int32_t sc[16];
-      scores(g0 + t, sc);
+      load_k(g0 + t, kr[0]);
+      scores(g0 + t, kr[0], sc);
 #pragma unroll
       for (int j = 0; j < 16; ++j) rowmax = max(rowmax, sc[j]);
     }
@@ -1034,7 +1074,8 @@ __global__ __launch_bounds__(192) void attn_kernel(AttnArgs a) {
 #pragma unroll 1
     for (int t = 0; t < ntile; ++t) {
       int32_t sc[16];
-      scores(g0 + t, sc);
+      load_k(g0 + t, kr[0]);
+      scores(g0 + t, kr[0], sc);
 #pragma unroll
       for (int j = 0; j < 16; ++j) Z += expo(g0 + t, j, sc[j], rowmax);
     }
@@ -1042,10 +1083,12 @@ __global__ __launch_bounds__(192) void attn_kernel(AttnArgs a) {
 #pragma unroll 1
     for (int t = 0; t < ntile; ++t) {
       int32_t sc[16];
-      scores(g0 + t, sc);
+      load_k(g0 + t, kr[0]);
+      load_v(g0 + t, vf[0]);
+      scores(g0 + t, kr[0], sc);
 #pragma unroll
       for (int j = 0; j < 16; ++j) sc[j] = expo(g0 + t, j, sc[j], rowmax);
-      pv(g0 + t, sc);
+      pv(vf[0], sc);
     }
   }
   SP += __shfl_xor(SP, 32);
@@ -1174,7 +1217,10 @@ hipError_t attention(const AttnArgs& a, hipStream_t s) {
   if (!a.vt || a.shift_s < 1 || a.shift_s > 30 || a.max_kt < 1) return hipErrorInvalidValue;
   const dim3 grid(a.B, kNKV, (a.max_T + 31) / 32), block(192);
   // up to 8 key tiles (256 keys) the scores stay in registers; beyond, every pass recomputes them
-  if (a.max_kt <= 8) {
+  if (a.max_kt <= 5) {
+    if (a.bits_c == 16) hipLaunchKernelGGL((attn_kernel<2, 5>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((attn_kernel<4, 5>), grid, block, 0, s, a);
+  } else if (a.max_kt <= 8) {
     if (a.bits_c == 16) hipLaunchKernelGGL((attn_kernel<2, 8>), grid, block, 0, s, a);
     else hipLaunchKernelGGL((attn_kernel<4, 8>), grid, block, 0, s, a);
   } else {

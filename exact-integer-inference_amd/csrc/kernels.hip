@@ -89,12 +89,16 @@ __device__ __forceinline__ v16i mfma32(v4i a, v4i b, v16i c) {
 // D[m][n] = sum_k a[m,k] W[n,k].  Lane = 32 h + c, register j = 4 b + r holds row
 // i = 8 b + 4 h + r, column c of the 32x32 tile: the 32 lanes of a half-wave hold 32
 // consecutive columns of one row, so every epilogue store is a contiguous run.
-template <int AW>
+// NARROW: 64 x 192 tiles for N a multiple of 192 but not of 128 (N = 576: three column blocks
+// instead of four and a half, so the persistent workgroups get evenly sized tiles and no
+// half-empty ones), 2-limb activations only.
+template <int AW, bool NARROW = false>
 struct GemmCfg {
+  static_assert(!NARROW || AW == 2, "narrow tiles for 2-limb activations");
   static constexpr int kThreads = 256;                   // 4 waves; two workgroups share a CU
-  static constexpr int BM = AW == 2 ? 128 : 64, BN = 128;
-  static constexpr int WM = BM / 2, WN = 64;             // 2 x 2 waves
-  static constexpr int TM = WM / 32, TN = 2;             // 32x32 tiles per wave
+  static constexpr int BM = AW == 2 && !NARROW ? 128 : 64, BN = NARROW ? 192 : 128;
+  static constexpr int WM = BM / 2, WN = BN / 2;         // 2 x 2 waves
+  static constexpr int TM = WM / 32, TN = WN / 32;       // 32x32 tiles per wave
   static constexpr int kPlane = BM * kLdsRow;
   static constexpr int kStage = AW * kPlane;              // activation limb planes only: 16 KB
   static constexpr int kStages = 4;                       // loaded two and three steps ahead
@@ -115,9 +119,11 @@ __device__ __forceinline__ void tile_coords(int v, int nMB, int nNB, int& mb, in
 
 __device__ __forceinline__ uint32_t pack16(int32_t a, int32_t b) { return (uint32_t)(a & 0xFFFF) | ((uint32_t)b << 16); }
 
-template <int AW, int EPI, int NK>
+template <int AW, int EPI, int NK, bool NARROW>
 __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
-  using C = GemmCfg<AW>;
+  using C = GemmCfg<AW, NARROW>;
+  static_assert(!NARROW || EPI == EPI_RESID || EPI == EPI_I64 || EPI == EPI_REQ16 || EPI == EPI_REQ32 ||
+                EPI == EPI_LOGITS, "the SiLU and QKV epilogues pair columns 32 apart within 64-column blocks");
   static_assert(NK >= 1, "at least one K block");
   // EPI_SILU: entries 32768 - kTabHalf .. 32768 + kTabHalf - 1 of a 16-bit SiLU table as int16
   // after the stages (the gate values cluster around 0, so most table reads hit LDS)
@@ -534,7 +540,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
     __builtin_amdgcn_sched_group_barrier(0x100, C::TM * AW, 0);   // LDS reads
     __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);            // MFMA
     __builtin_amdgcn_sched_group_barrier(0x100, C::TM * AW, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, 4 * C::TM * AW - 2, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 2 * C::TM * AW * C::TN - 2, 0);
     // weights of st + 2, into the set this step just consumed
     w_step(CUR, jt + (kb + 2) / nk, (kb + 2) % nk);
     if (kb != nk - 1) return;
@@ -584,9 +590,9 @@ int device_cus() {
   return cus;
 }
 
-template <int AW, int EPI>
-hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
-  using C = GemmCfg<AW>;
+template <int AW, int EPI, bool NARROW>
+hipError_t launch_gemm_cfg(const GemmArgs& a, hipStream_t s) {
+  using C = GemmCfg<AW, NARROW>;
   const int nT = ((a.M + C::BM - 1) / C::BM) * ((a.N + C::BN - 1) / C::BN);
   // two persistent workgroups per CU, a multiple of 8 so every XCD gets the same count
   const int per_xcd = std::min((nT + 7) / 8, std::max(1, 2 * device_cus() / 8));
@@ -595,15 +601,22 @@ hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
   // (576, 1536) for every epilogue, and 64, 128 for the operator entry points
   constexpr bool op = EPI == EPI_I64 || EPI == EPI_REQ16 || EPI == EPI_REQ32;
   switch (a.K / kBK) {
-    case 9: hipLaunchKernelGGL((gemm_kernel<AW, EPI, 9>), grid, block, 0, s, a); break;
-    case 24: hipLaunchKernelGGL((gemm_kernel<AW, EPI, 24>), grid, block, 0, s, a); break;
-    case 1: if constexpr (op) { hipLaunchKernelGGL((gemm_kernel<AW, EPI, 1>), grid, block, 0, s, a); break; }
+    case 9: hipLaunchKernelGGL((gemm_kernel<AW, EPI, 9, NARROW>), grid, block, 0, s, a); break;
+    case 24: hipLaunchKernelGGL((gemm_kernel<AW, EPI, 24, NARROW>), grid, block, 0, s, a); break;
+    case 1: if constexpr (op) { hipLaunchKernelGGL((gemm_kernel<AW, EPI, 1, NARROW>), grid, block, 0, s, a); break; }
             return hipErrorInvalidValue;
-    case 2: if constexpr (op) { hipLaunchKernelGGL((gemm_kernel<AW, EPI, 2>), grid, block, 0, s, a); break; }
+    case 2: if constexpr (op) { hipLaunchKernelGGL((gemm_kernel<AW, EPI, 2, NARROW>), grid, block, 0, s, a); break; }
             return hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+template <int AW, int EPI>
+hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
+  if constexpr (AW == 2 && EPI == EPI_RESID)
+    if (a.N % 192 == 0 && a.N % 128 != 0) return launch_gemm_cfg<AW, EPI, true>(a, s);
+  return launch_gemm_cfg<AW, EPI, false>(a, s);
 }
 
 template <int W>

@@ -53,12 +53,12 @@ __device__ __forceinline__ uint32_t limb_word(const int32_t* v, int l, int W) {
 }
 
 // ------------------------------------------------------------------------------ GEMM
-// Persistent workgroups of 4 waves (two per CU, so one's epilogue overlaps the other's MFMA loop)
-// sweep BM x 128 output tiles (BM = 128 for 2-limb activations, 64 for 4-limb) in a flat
-// (tile, K block of 64) loop.  Activation limb planes pass through two LDS stages; each wave
-// loads its weight fragments straight into registers (the weights are L2-resident), both two
-// steps ahead.  v_mfma_i32_32x32x32_i8 sustains about twice the int8 rate of the 16x16x64 form
-// on gfx950.
+// Persistent workgroups of 4 waves, two per CU, sweep BM x BN output tiles (128 x 128 for 2-limb
+// activations, 64 x 128 for 4-limb, 64 x 192 for 2-limb residual GEMMs with N = 576) in a flat
+// (tile, K block of 64) loop.  Activation limb planes go global -> LDS through 4-8 stages;
+// each wave loads its weight fragments straight into registers (the weights are L2-resident)
+// two steps ahead.  v_mfma_i32_32x32x32_i8 sustains about twice the int8 rate of the 16x16x64
+// form on gfx950.
 //
 // Epilogue arithmetic for 2-limb inputs runs in float64 and is exact: with P1, P0 the limb
 // partial sums (|P| < 2^25 for K <= 1536) and |m| <= 2^14,

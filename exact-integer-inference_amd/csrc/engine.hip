@@ -113,6 +113,18 @@ struct eii_model {
   size_t ev_used = 0;
 };
 
+// KV cache of incremental decoding: per layer the q|k|v rows (int16 [B cap][960], row b cap + t
+// = position t of sequence b) and the V^T limb planes of those rows (vt_stride_for(B cap)).
+struct eii_kv {
+  int device = 0;
+  int B = 0, cap = 0;              // sequences, positions per sequence (a multiple of 32)
+  int len = 0;                     // positions held by every sequence
+  uint8_t* dev = nullptr;          // one allocation for all layers
+  int16_t* qkv[kNL] = {};
+  uint8_t* vt[kNL] = {};
+  int32_t* seq_off = nullptr;      // [B + 1] = b cap
+};
+
 namespace {
 // Records a start and stop event around the launches made in its scope, on their stream.
 struct ProfScope {
@@ -544,7 +556,14 @@ hipError_t copy_cols(void* dst, int dst_w, const void* src, int src_w, int col0,
 // context and the gated product live in m->h, m->ctx and m->gated as int8 limb planes; with a
 // trace the unfused q/k/v and gate/up projections run so their values can be dumped, and the
 // producers also write plain copies into the trace buffers.
-int run_block(eii_model* m, int l, int32_t* x, int M, int nseq, int max_T, const eii_trace* tr, hipStream_t s) {
+// One step of incremental decoding: T_new new positions of every sequence, from position p0.
+struct KvStep {
+  eii_kv* kv;
+  int T_new, p0;
+};
+
+int run_block(eii_model* m, int l, int32_t* x, int M, int nseq, int max_T, const eii_trace* tr, hipStream_t s,
+              const KvStep* kv = nullptr) {
   const Layer& L = m->L[l];
   const int hb = L.bits[NORM1] / 8;
   uint8_t* h = (uint8_t*)m->h;
@@ -558,8 +577,10 @@ int run_block(eii_model* m, int l, int32_t* x, int M, int nseq, int max_T, const
     GemmArgs g = gemm_args(L.qkv, h, M, m->qkv, 16);
     if (!tr) {   // q, k, v projections with RoPE and the V^T planes in the epilogue
       g.pos = m->pos; g.cosT = m->rope_c; g.sinT = m->rope_s; g.sh_q = sh_q; g.sh_k = sh_k;
-      g.vt = m->vt; g.vt_stride = vt_stride_for(M);
+      if (!kv) { g.vt = m->vt; g.vt_stride = vt_stride_for(M); }
       HIPCHK(gemm(g, hb, EPI_QKV, s));
+      // decoding: the new rows join the cache, whose V^T planes take their v columns
+      if (kv) HIPCHK(kv_append(m->qkv, nseq, kv->T_new, kv->kv->cap, kv->p0, kv->kv->qkv[l], kv->kv->vt[l], s));
     } else {
       HIPCHK(gemm(g, hb, EPI_REQ16, s));
     }
@@ -578,6 +599,17 @@ int run_block(eii_model* m, int l, int32_t* x, int M, int nseq, int max_T, const
     ProfScope ps(m, EII_K_ATTN, s);
     AttnArgs a{m->qkv, m->vt, m->seq_off, m->exp_tab, tr ? tr->attn_ctx : nullptr, (uint8_t*)m->ctx, M, nseq, max_T,
                m->max_kt, L.f[QR] + L.f[KR] + 3 - kFScore, 16 + L.f[VP] - L.f[CTX], L.bits[CTX]};
+    if (kv) {   // queries of the new positions against every cached key
+      const int len = kv->p0 + kv->T_new;
+      a.qkv = kv->kv->qkv[l];
+      a.vt = kv->kv->vt[l];
+      a.seq_off = kv->kv->seq_off;
+      a.M = nseq * kv->kv->cap;
+      a.max_T = a.kv_len = len;
+      a.max_kt = (len + 31) / 32;
+      a.q_first = kv->p0;
+      a.out_M = M;
+    }
     HIPCHK(attention(a, s));
   }
   {
@@ -677,6 +709,90 @@ extern "C" int eii_forward_packed(eii_model* m, const int64_t* ids, const int32_
   if (!m || !ids || !seq_lens || nseq <= 0) return fail(EII_E_ARG, "bad forward arguments");
   std::vector<int32_t> lens(seq_lens, seq_lens + nseq);
   return forward_impl(m, ids, lens, emb_out, res_out, logits, (hipStream_t)stream);
+}
+
+// ------------------------------------------------------------------------------ decoding
+extern "C" int eii_kv_create(eii_model* m, int B, int max_T, eii_kv** out) {
+  if (!m || !out || B <= 0 || max_T <= 0) return fail(EII_E_ARG, "bad kv cache arguments");
+  *out = nullptr;
+  if (max_T > 16384) return fail(EII_E_BOUND, "sequences longer than 16384 tokens are not supported");
+  const int cap = (max_T + 31) / 32 * 32;
+  if ((size_t)B * cap > ((size_t)1 << 22)) return fail(EII_E_ARG, "more than 4194304 cached positions");
+  HIPCHK(hipSetDevice(m->device));
+  auto al256 = [](size_t n) { return (n + 255) & ~(size_t)255; };
+  const size_t rows = (size_t)B * cap, qb = al256(rows * kQKVN * 2), vb = al256(vt_bytes((int)rows));
+  eii_kv* kv = new eii_kv;
+  kv->device = m->device;
+  kv->B = B;
+  kv->cap = cap;
+  if (hipMalloc(&kv->dev, kNL * (qb + vb) + al256((size_t)(B + 1) * 4)) != hipSuccess) {
+    delete kv;
+    return fail(EII_E_DEVICE, "kv cache allocation failed");
+  }
+  for (int l = 0; l < kNL; ++l) {
+    kv->qkv[l] = (int16_t*)(kv->dev + l * (qb + vb));
+    kv->vt[l] = kv->dev + l * (qb + vb) + qb;
+  }
+  kv->seq_off = (int32_t*)(kv->dev + kNL * (qb + vb));
+  std::vector<int32_t> off(B + 1);
+  for (int b = 0; b <= B; ++b) off[b] = b * cap;
+  if (hipMemcpy(kv->seq_off, off.data(), off.size() * 4, hipMemcpyHostToDevice) != hipSuccess) {
+    (void)hipFree(kv->dev);
+    delete kv;
+    return fail(EII_E_DEVICE, "kv cache upload failed");
+  }
+  *out = kv;
+  return EII_OK;
+}
+
+extern "C" void eii_kv_free(eii_kv* kv) {
+  if (!kv) return;
+  (void)hipSetDevice(kv->device);
+  (void)hipFree(kv->dev);
+  delete kv;
+}
+
+extern "C" int eii_kv_length(const eii_kv* kv) { return kv ? kv->len : 0; }
+
+extern "C" int eii_kv_reset(eii_kv* kv) {
+  if (!kv) return fail(EII_E_ARG, "null kv cache");
+  kv->len = 0;
+  return EII_OK;
+}
+
+extern "C" int eii_kv_append(eii_model* m, eii_kv* kv, const int64_t* ids, int T_new, int32_t* logits, void* stream) {
+  if (!m || !kv || !ids || T_new <= 0) return fail(EII_E_ARG, "bad kv append arguments");
+  if (kv->device != m->device) return fail(EII_E_ARG, "kv cache and model on different devices");
+  const int p0 = kv->len, len = p0 + T_new;
+  if (len > kv->cap)
+    return fail(EII_E_BOUND, "the kv cache holds " + std::to_string(kv->cap) + " positions per sequence");
+  if (len > m->rope_rows)
+    return fail(EII_E_BOUND, "position " + std::to_string(len - 1) + " beyond the " + std::to_string(m->rope_rows) +
+                                 " RoPE rows loaded (eii_model_set_rope)");
+  const size_t M = (size_t)kv->B * T_new;
+  if (M > ((size_t)1 << 22)) return fail(EII_E_ARG, "more than 4194304 rows in one append");
+  HIPCHK(hipSetDevice(m->device));
+  hipStream_t s = (hipStream_t)stream;
+  int rc;
+  if ((rc = ensure_ws(m, M))) return rc;
+  HIPCHK(fill_positions(m->pos, kv->B, T_new, p0, s));
+  m->last_lens.clear();   // the positions no longer belong to the last plain batch
+  {
+    ProfScope ps(m, EII_K_EMBED, s);
+    HIPCHK(embed(ids, (int)M, m->emb_q, m->emb_m, m->emb_sh, m->x, m->flags, s));
+  }
+  const KvStep step{kv, T_new, p0};
+  for (int l = 0; l < kNL; ++l)
+    if ((rc = run_block(m, l, m->x, (int)M, kv->B, len, nullptr, s, &step))) return rc;
+  kv->len = len;
+  if (logits) return run_final(m, m->x, (int)M, logits, s);
+  return EII_OK;
+}
+
+extern "C" int eii_argmax(const int32_t* logits, int rows, int n, int64_t* out, void* stream) {
+  if (!logits || !out || rows <= 0 || n <= 0) return fail(EII_E_ARG, "bad argmax arguments");
+  HIPCHK(argmax_rows(logits, rows, n, out, (hipStream_t)stream));
+  return EII_OK;
 }
 
 extern "C" int eii_profile_begin(eii_model* m, int max_launches) {

@@ -108,9 +108,23 @@ struct AttnArgs {
   int shift_s;             // f_qr + f_kr + 3 - 7, >= 1
   int sh_ctx;              // 16 + f_v - f_c
   int bits_c;
+  // Incremental decoding over a KV cache (kv_len = 0: a plain forward).  Sequence b holds kv_len
+  // tokens at rows seq_off[b] ..; only query positions q_first .. kv_len - 1 are computed, and
+  // the context of position t goes to row b (kv_len - q_first) + t - q_first of the ctx outputs,
+  // which have out_M rows.
+  int kv_len = 0, q_first = 0, out_M = 0;
 };
 // 32-row key tiles (aligned to multiples of 32 rows) spanned by a sequence at rows [s0, s0 + T)
 inline int attn_key_tiles(int s0, int T) { return ((s0 + T - 1) >> 5) - (s0 >> 5) + 1; }
 hipError_t attention(const AttnArgs& a, hipStream_t s);
+
+// KV cache append: rows b T_new + i of qkv [B T_new, 960] go to row b cap + p0 + i of the cache
+// rows and, for the v columns, to the cache's V^T limb planes (vt_stride_for(B cap))
+hipError_t kv_append(const int16_t* qkv, int B, int T_new, int cap, int p0, int16_t* cache_qkv, uint8_t* cache_vt,
+                     hipStream_t s);
+// pos[b T_new + i] = p0 + i
+hipError_t fill_positions(int32_t* pos, int B, int T_new, int p0, hipStream_t s);
+// out[r] = the lowest index of the largest of the n values of row r
+hipError_t argmax_rows(const int32_t* v, int rows, int n, int64_t* out, hipStream_t s);
 
 }  // namespace eii

@@ -822,8 +822,8 @@ __global__ __launch_bounds__(192) __attribute__((amdgpu_waves_per_eu(2))) void a
   __shared__ __attribute__((aligned(16))) int32_t skl[3][32];   // per wave: 128 * sum_d k per key
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, c = lane & 31, h = lane >> 5;
-  const int seq = blockIdx.x, kvg = blockIdx.y, qt = gridDim.z - 1 - blockIdx.z;
-  const int s0 = a.seq_off[seq], T = a.seq_off[seq + 1] - s0;
+  const int seq = blockIdx.x, kvg = blockIdx.y, qt = (a.q_first >> 5) + gridDim.z - 1 - blockIdx.z;
+  const int s0 = a.seq_off[seq], T = a.kv_len ? a.kv_len : a.seq_off[seq + 1] - s0;
   if (32 * qt >= T) return;
   for (int i = tid; i < kDMax + 2; i += 192) etab[i] = i <= kDMax ? a.exp_tab[i] : 0;
   __syncthreads();
@@ -1106,9 +1106,11 @@ __global__ __launch_bounds__(192) __attribute__((amdgpu_waves_per_eu(2))) void a
   }
   SP += __shfl_xor(SP, 32);
 
-  if (qi > qlast) return;
+  if (qi > qlast || qi - s0 < a.q_first) return;
   // ctx of query qi, d = 32 dt + 8 b + 4 h + r (output register 4 b + r of tile dt)
-  const size_t orow = (size_t)qi * kD + hh * 64, pl = (size_t)a.M * kD;
+  const int outM = a.kv_len ? a.out_M : a.M;
+  const int qo = a.kv_len ? seq * (T - a.q_first) + qi - s0 - a.q_first : qi;   // output row
+  const size_t orow = (size_t)qo * kD + hh * 64, pl = (size_t)outM * kD;
 #pragma unroll
   for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
@@ -1124,7 +1126,7 @@ __global__ __launch_bounds__(192) __attribute__((amdgpu_waves_per_eu(2))) void a
       if (a.ctx_planes) {
 #pragma unroll
         for (int l = 0; l < OB; ++l)
-          *(uint32_t*)(a.ctx_planes + l * pl + plane_offset(qi, hh * 64 + d0, a.M)) = limb_word(cv, l, OB);
+          *(uint32_t*)(a.ctx_planes + l * pl + plane_offset(qo, hh * 64 + d0, outM)) = limb_word(cv, l, OB);
       }
       if (a.ctx) {
         if constexpr (OB == 2) *(uint2*)((int16_t*)a.ctx + orow + d0) = make_uint2(pack16(cv[0], cv[1]), pack16(cv[2], cv[3]));
@@ -1228,7 +1230,11 @@ hipError_t silu_gate(const int16_t* gu, int M, const int32_t* silu, int sh, int 
 hipError_t attention(const AttnArgs& a, hipStream_t s) {
   if (a.B <= 0 || a.max_T <= 0) return hipSuccess;
   if (!a.vt || a.shift_s < 1 || a.shift_s > 30 || a.max_kt < 1) return hipErrorInvalidValue;
-  const dim3 grid(a.B, kNKV, (a.max_T + 31) / 32), block(192);
+  if (a.kv_len && (a.q_first < 0 || a.q_first >= a.kv_len || a.max_T != a.kv_len ||
+                   a.out_M != a.B * (a.kv_len - a.q_first)))
+    return hipErrorInvalidValue;
+  // query tiles from the one holding q_first (0 for a plain forward) to the end
+  const dim3 grid(a.B, kNKV, (a.max_T + 31) / 32 - (a.q_first >> 5)), block(192);
   // up to 8 key tiles (256 keys) the scores stay in registers; beyond, every pass recomputes them
   if (a.max_kt <= 5) {
     if (a.bits_c == 16) hipLaunchKernelGGL((attn_kernel<2, 5>), grid, block, 0, s, a);
@@ -1240,6 +1246,76 @@ hipError_t attention(const AttnArgs& a, hipStream_t s) {
     if (a.bits_c == 16) hipLaunchKernelGGL((attn_kernel<2, 0>), grid, block, 0, s, a);
     else hipLaunchKernelGGL((attn_kernel<4, 0>), grid, block, 0, s, a);
   }
+  return hipGetLastError();
+}
+
+// KV cache append: thread = (new row, one of the 960 columns); the v columns also write their two
+// V^T limb bytes (low byte - 128, signed high byte) at the row's cache column
+__global__ __launch_bounds__(256) void kv_append_kernel(const int16_t* qkv, int B, int T_new, int cap, int p0,
+                                                         int16_t* cache, uint8_t* vt, int stride) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (size_t)B * T_new * kQKVN) return;
+  const int r = (int)(i / kQKVN), col = (int)(i % kQKVN), b = r / T_new, t = r % T_new;
+  const size_t crow = (size_t)b * cap + p0 + t;
+  const int16_t v = qkv[i];
+  cache[crow * kQKVN + col] = v;
+  if (col >= kD + 192) {
+    const size_t d = col - kD - 192;
+    vt[d * stride + crow] = (uint8_t)((uint32_t)v ^ 0x80u);
+    vt[(size_t)192 * stride + d * stride + crow] = (uint8_t)((uint32_t)v >> 8);
+  }
+}
+
+hipError_t kv_append(const int16_t* qkv, int B, int T_new, int cap, int p0, int16_t* cache_qkv, uint8_t* cache_vt,
+                     hipStream_t s) {
+  if (B <= 0 || T_new <= 0 || p0 < 0 || p0 + T_new > cap) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(kv_append_kernel, dim3(blocks_for((size_t)B * T_new * kQKVN)), dim3(256), 0, s, qkv, B, T_new,
+                     cap, p0, cache_qkv, cache_vt, vt_stride_for(B * cap));
+  return hipGetLastError();
+}
+
+__global__ __launch_bounds__(256) void fill_pos_kernel(int32_t* pos, int n, int T_new, int p0) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) pos[i] = p0 + i % T_new;
+}
+
+hipError_t fill_positions(int32_t* pos, int B, int T_new, int p0, hipStream_t s) {
+  const int n = B * T_new;
+  hipLaunchKernelGGL(fill_pos_kernel, dim3((n + 255) / 256), dim3(256), 0, s, pos, n, T_new, p0);
+  return hipGetLastError();
+}
+
+// one workgroup per row: each thread scans a strided slice keeping (value, lowest index), then
+// a tree reduction in LDS that prefers the lower index on equal values
+__global__ __launch_bounds__(256) void argmax_kernel(const int32_t* v, int n, int64_t* out) {
+  __shared__ int32_t bv[256];
+  __shared__ int32_t bi[256];
+  const int32_t* row = v + (size_t)blockIdx.x * n;
+  int32_t best = INT32_MIN;
+  int32_t bidx = n;
+  for (int j = threadIdx.x; j < n; j += 256) {
+    const int32_t x = row[j];
+    if (x > best || bidx == n) { best = x; bidx = j; }
+  }
+  bv[threadIdx.x] = best;
+  bi[threadIdx.x] = bidx;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if (threadIdx.x < w) {
+      const int32_t ov = bv[threadIdx.x + w], oi = bi[threadIdx.x + w];
+      if (oi < n && (bi[threadIdx.x] == n || ov > bv[threadIdx.x] || (ov == bv[threadIdx.x] && oi < bi[threadIdx.x]))) {
+        bv[threadIdx.x] = ov;
+        bi[threadIdx.x] = oi;
+      }
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) out[blockIdx.x] = bi[0];
+}
+
+hipError_t argmax_rows(const int32_t* v, int rows, int n, int64_t* out, hipStream_t s) {
+  if (rows <= 0 || n <= 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(argmax_kernel, dim3(rows), dim3(256), 0, s, v, n, out);
   return hipGetLastError();
 }
 

@@ -135,6 +135,35 @@ class Engine:
         self.check()
         return lg
 
+    # ------------------------------------------------------------------ decoding
+    def kv_cache(self, B, max_T):
+        """A KV cache for incremental decoding of B sequences of up to max_T positions."""
+        return KVCache(self, B, max_T)
+
+    def argmax(self, logits):
+        """int64 [rows]: the lowest index of each row's largest logit (numpy.argmax's tie rule)."""
+        lg = logits.reshape(-1, logits.shape[-1]).contiguous()
+        out = torch.empty(lg.shape[0], dtype=torch.int64, device=self.device)
+        L.check(self.lib.eii_argmax(_ptr(lg), lg.shape[0], lg.shape[1], _ptr(out), _stream()))
+        return out
+
+    def generate(self, prompt, n):
+        """Greedy continuation of n tokens after prompt int64 [B, T0] with a KV cache; returns
+        (tokens int64 [B, n], logits of every position int32 [B, T0 + n - 1, 49152] on the device)."""
+        prompt = self._ids(prompt)
+        B, T0 = prompt.shape
+        self.ensure_rope(T0 + n)
+        kv = self.kv_cache(B, T0 + n)
+        try:
+            logits = [kv.append(prompt)]
+            toks = [self.argmax(logits[-1][:, -1])]
+            for _ in range(n - 1):
+                logits.append(kv.append(toks[-1][:, None]))
+                toks.append(self.argmax(logits[-1][:, -1]))
+        finally:
+            kv.close()
+        return torch.stack(toks, dim=1), torch.cat(logits, dim=1)
+
     # ------------------------------------------------------------------ helpers
     def _ids(self, ids):
         if isinstance(ids, np.ndarray):
@@ -161,3 +190,53 @@ class Engine:
         for k, v in out.items():
             r[k] = v.view(NL, B, T, -1) if k == "resid" else v.view(B, T, -1)
         return r
+
+
+class KVCache:
+    """Incremental decoding state on an Engine's device: per layer the q|k|v rows and V^T planes of
+    every position appended so far, for B sequences of up to max_T positions.
+
+    No counterpart in python/intref.py, whose forward recomputes every position over the full
+    prefix; the cache is the reference's stated next step (exact-integer-inference.tex:167).  Each
+    position depends only on its prefix, so appended positions get the logits a full forward over
+    the whole sequence gives them.
+    """
+
+    def __init__(self, engine, B, max_T):
+        self.engine = engine
+        self.B = B
+        engine.ensure_rope(max_T)
+        h = C.c_void_p()
+        L.check(engine.lib.eii_kv_create(engine.h, B, max_T, C.byref(h)))
+        self.h = h
+
+    @property
+    def length(self):
+        return self.engine.lib.eii_kv_length(self.h)
+
+    def reset(self):
+        L.check(self.engine.lib.eii_kv_reset(self.h))
+
+    def append(self, ids, logits=True, check=True):
+        """ids int64 [B, T_new] -> logits int32 [B, T_new, 49152] of the new positions (or None)."""
+        e = self.engine
+        ids = e._ids(ids)
+        if ids.shape[0] != self.B:
+            raise L.EIIError(L.EII_E_ARG, f"expected {self.B} sequences, got {ids.shape[0]}")
+        T_new = ids.shape[1]
+        lg = torch.empty((self.B, T_new, V), dtype=torch.int32, device=e.device) if logits else None
+        L.check(e.lib.eii_kv_append(e.h, self.h, _ptr(ids), T_new, _ptr(lg), _stream()))
+        if check:
+            e.check()
+        return lg
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.engine.lib.eii_kv_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

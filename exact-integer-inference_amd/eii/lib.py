@@ -40,6 +40,12 @@ SIGNATURES = {
     "eii_forward": (i32, [vp, vp, i32, i32, vp, vp, vp, vp]),
     "eii_forward_packed": (i32, [vp, vp, i32p, i32, vp, vp, vp, vp]),
     "eii_check": (i32, [vp, vp]),
+    "eii_kv_create": (i32, [vp, i32, i32, C.POINTER(vp)]),
+    "eii_kv_free": (None, [vp]),
+    "eii_kv_length": (i32, [vp]),
+    "eii_kv_reset": (i32, [vp]),
+    "eii_kv_append": (i32, [vp, vp, vp, i32, vp, vp]),
+    "eii_argmax": (i32, [vp, i32, i32, vp, vp]),
     "eii_profile_begin": (i32, [vp, i32]),
     "eii_profile_end": (i32, [vp, vp, C.POINTER(C.c_double), i32p]),
     "eii_block": (i32, [vp, i32, vp, i32, i32, C.POINTER(eii_trace), vp]),

@@ -96,6 +96,27 @@ int eii_profile_begin(eii_model* m, int max_launches);
  * into ms[EII_K_COUNT] and launches[EII_K_COUNT]; status 5 if launches were dropped. */
 int eii_profile_end(eii_model* m, void* stream, double* ms, int* launches);
 
+/* ---- incremental decoding with a KV cache ----
+ * No counterpart in the reference, whose forward recomputes every position over the full prefix;
+ * the cache is its stated next step (exact-integer-inference.tex:167, docs/CONFORMANCE.md:11).
+ * Each position depends only on its prefix, so the logits of appended positions equal the rows
+ * of a full forward (eii_forward) over the whole sequence. */
+typedef struct eii_kv eii_kv;
+
+/* A cache for B sequences of up to max_T positions each (q|k|v rows and V^T planes per layer). */
+int eii_kv_create(eii_model* m, int B, int max_T, eii_kv** out);
+void eii_kv_free(eii_kv* kv);
+/* Positions held by every sequence; eii_kv_reset empties the cache. */
+int eii_kv_length(const eii_kv* kv);
+int eii_kv_reset(eii_kv* kv);
+/* Appends T_new positions to every sequence: ids_dev int64 [B, T_new]; logits_dev int32
+ * [B, T_new, 49152] (nullable) receives their logits.  A prompt is one append of its length,
+ * each decoding step an append of 1.  After an error the cache contents are undefined: reset it. */
+int eii_kv_append(eii_model* m, eii_kv* kv, const int64_t* ids_dev, int T_new, int32_t* logits_dev, void* stream);
+/* Greedy choice: out_dev int64 [rows] = the lowest index of the largest of the n values of each row of
+ * logits_dev int32 [rows, n] (numpy.argmax's tie rule). */
+int eii_argmax(const int32_t* logits_dev, int rows, int n, int64_t* out_dev, void* stream);
+
 /* ---- operator level (python/intref.py functions) ---- */
 
 /* Row sums of int8 weights W_dev [N, K] into wsum_dev int32 [N]. */

@@ -140,3 +140,31 @@ def ensure_model(kind="base"):
 def rope_sidecar(T):
     """(cos, sin) int64 [T, 32] RoPE tables for positions beyond model.bin's 512 rows."""
     return rope_tables(T)
+
+
+def make_float_checkpoint(path, seed=0):
+    """A bfloat16 model.safetensors with the tensor names and shapes of SmolLM2-135M (the names
+    python/common.py:50-68 reads) and random values at the real model's scales: matrices with
+    standard deviation 1/sqrt(K), norm gains around 1.  Input of the real-weight path when the
+    checkpoint itself is absent."""
+    import torch
+    from safetensors.torch import save_file
+    g = torch.Generator().manual_seed(seed)
+
+    def mat(n, k):
+        return (torch.randn((n, k), generator=g) / math.sqrt(k)).to(torch.bfloat16)
+
+    def gain(n):
+        return (1.0 + 0.1 * torch.randn((n,), generator=g)).to(torch.bfloat16)
+
+    t = {"model.embed_tokens.weight": mat(mb.V, mb.D), "model.norm.weight": gain(mb.D)}
+    for l in range(mb.NL):
+        p = f"model.layers.{l}."
+        t[p + "input_layernorm.weight"] = gain(mb.D)
+        t[p + "post_attention_layernorm.weight"] = gain(mb.D)
+        for name, key in (("q", "self_attn.q_proj"), ("k", "self_attn.k_proj"), ("v", "self_attn.v_proj"),
+                          ("o", "self_attn.o_proj"), ("gate", "mlp.gate_proj"), ("up", "mlp.up_proj"),
+                          ("down", "mlp.down_proj")):
+            t[p + key + ".weight"] = mat(*mb.MAT_NK[name])
+    save_file(t, path)
+    return path

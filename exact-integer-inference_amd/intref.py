@@ -52,8 +52,7 @@ def sat(x, bits):                 # python/intref.py:53-55
     return np.clip(x, lo, hi)
 
 
-def dequant(q, f):                # python/intref.py:311
-    return np.asarray(q, dtype=np.float64) * 2.0 ** (-f)
+from eii.quant import dequant   # noqa: E402  python/intref.py:311
 
 
 def exp_table():                  # python/intref.py:72-77
@@ -70,22 +69,8 @@ def rope_tables(T, theta=100000, head_dim=64):   # python/intref.py:96-108
     return _tables.rope_tables(T)
 
 
-def quant_rows(W):                # python/intref.py:113-124
-    """W float [N, K] -> (q int8-valued float64 [N, K], m int64 [N], n int64 [N]); scale m 2^-n."""
-    W = np.asarray(W, dtype=np.float64)
-    s = np.abs(W).max(1) / 127.0
-    s = np.where(s == 0, 1.0, s)
-    n = (13 - np.floor(np.log2(s))).astype(I64)
-    m = np.rint(s * 2.0 ** n).astype(I64)
-    assert m.min() >= 2 ** 13 and m.max() <= 2 ** 14
-    sw = m * 2.0 ** (-n.astype(np.float64))
-    return np.clip(np.rint(W / sw[:, None]), -127, 127), m, n
-
-
-def quant_vec_int16(w):           # python/intref.py:127-130
-    w = np.asarray(w, dtype=np.float64)
-    f = 14 - int(math.floor(math.log2(np.abs(w).max())))
-    return np.clip(np.rint(w * 2.0 ** f), -32768, 32767).astype(I64), f
+# quant_rows (python/intref.py:113-124), quant_vec_int16 (:127-130): eii/quant.py
+from eii.quant import quant_rows, quant_vec_int16   # noqa: E402
 
 
 # ---------------------------------------------------------------- GPU operators

@@ -959,6 +959,8 @@ extern "C" int eii_linear(const void* A, int a_bits, const int8_t* W, const int3
 extern "C" int eii_rmsnorm(const int32_t* x, int M, const int32_t* gain, int f_gain, int f_out, int out_bits,
                            void* out, void* stream) {
   if (!x || !gain || !out || M <= 0) return fail(EII_E_ARG, "bad rmsnorm arguments");
+  // the kernel moves 4 columns per access
+  if (((uintptr_t)x | (uintptr_t)gain | (uintptr_t)out) & 15) return fail(EII_E_ARG, "x, gain and out must be 16-byte aligned");
   if (out_bits != 16 && out_bits != 32) return fail(EII_E_ARG, "out_bits must be 16 or 32");
   int rc;
   if ((rc = check_scalar_shift(21 + f_gain - f_out, "norm"))) return rc;

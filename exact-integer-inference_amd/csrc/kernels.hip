@@ -691,59 +691,66 @@ __global__ __launch_bounds__(256) void embed_kernel(const int64_t* ids, int M, c
 template <int OB>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const int32_t* x, int M, const int32_t* gain,
                                                       int sh_out, int bits_out, uint8_t* planes, void* plain) {
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-  if (row >= M) return;
-  const int32_t* xr = x + (size_t)row * kD;
-  int32_t v[9], g3[9];
+  // 16 lanes per row, 4 rows per wave: lane c of a row holds columns 64 k + 4 c .. + 3, k = 0..8,
+  // so loads are 16 bytes, the limb bytes of 4 columns leave as one dword, the row sums reduce in
+  // 4 steps inside the 16-lane group and each lane evaluates its own row's U
+  const int row = blockIdx.x * 16 + (threadIdx.x >> 4), c = threadIdx.x & 15;
+  const int rowc = min(row, M - 1);   // rows past M compute on row M - 1 and store nothing
+  const int32_t* xr = x + (size_t)rowc * kD + 4 * c;
+  int4 v[9], g3[9];
   int64_t A = 0, B = 0, Cs = 0;
 #pragma unroll
-  for (int j = 0; j < 9; ++j) {
-    v[j] = xr[lane + 64 * j];
-    g3[j] = gain[lane + 64 * j];
+  for (int k = 0; k < 9; ++k) {
+    v[k] = *(const int4*)(xr + 64 * k);
+    g3[k] = *(const int4*)(gain + 64 * k + 4 * c);
   }
 #pragma unroll
-  for (int j = 0; j < 9; ++j) {
-    const int32_t hi = v[j] >> 16, lo = v[j] & 0xFFFF;
-    A += (int64_t)hi * hi; B += (int64_t)hi * lo; Cs += (int64_t)lo * lo;
-    g3[j] *= 3;
+  for (int k = 0; k < 9; ++k) {
+    const int32_t e[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int32_t hi = e[r] >> 16, lo = e[r] & 0xFFFF;
+      A += (int64_t)hi * hi; B += (int64_t)hi * lo; Cs += (int64_t)lo * lo;
+    }
+    g3[k].x *= 3; g3[k].y *= 3; g3[k].z *= 3; g3[k].w *= 3;
   }
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
+  for (int o = 8; o > 0; o >>= 1) {
     A += __shfl_xor(A, o); B += __shfl_xor(B, o); Cs += __shfl_xor(Cs, o);
   }
   const int32_t U = (int32_t)norm_U(norm_total(A, B, Cs));   // < 2^29
-  int32_t o[9];
-  if (sh_out >= 10 && sh_out <= 40) {
-    const int64_t rnd = (int64_t)1 << (sh_out - 1);
+  if (row >= M) return;
+  const size_t pl = (size_t)M * kD, m64 = (size_t)M * 64;
+  // the output shift is uniform: one copy of the loop per path
+  auto body = [&](auto FAST) __attribute__((always_inline)) {
+    const int64_t rnd = (int64_t)1 << (min(max(sh_out, 10), 40) - 1);
+    auto norm1 = [&](int32_t xv, int32_t gv) -> int32_t {
+      const int32_t z = (int32_t)(((int64_t)xv * U + 32768) >> 16);
+      if constexpr (decltype(FAST)::value) {
+        const int32_t q = (int32_t)(((int64_t)z * gv + rnd) >> sh_out);
+        return OB == 2 ? min(max(q, -32768), 32767) : q;
+      } else {
+        return (int32_t)sat(rs((int64_t)z * gv, sh_out), bits_out);
+      }
+    };
 #pragma unroll
-    for (int j = 0; j < 9; ++j) {
-      const int32_t z = (int32_t)(((int64_t)v[j] * U + 32768) >> 16);
-      const int32_t q = (int32_t)(((int64_t)z * g3[j] + rnd) >> sh_out);
-      o[j] = OB == 2 ? min(max(q, -32768), 32767) : q;
+    for (int k = 0; k < 9; ++k) {
+      const int32_t o[4] = {norm1(v[k].x, g3[k].x), norm1(v[k].y, g3[k].y), norm1(v[k].z, g3[k].z),
+                            norm1(v[k].w, g3[k].w)};
+      if (planes) {   // K-blocked planes: columns 64 k + 4 c .. + 3 of the row at k M 64 + row 64 + 4 c
+        uint8_t* pb = planes + k * m64 + (size_t)row * 64 + 4 * c;
+#pragma unroll
+        for (int l = 0; l < OB; ++l) *(uint32_t*)(pb + l * pl) = limb_word(o, l, OB);
+      }
+      if (plain) {
+        const size_t e = (size_t)row * kD + 64 * k + 4 * c;
+        if constexpr (OB == 2) *(uint2*)((int16_t*)plain + e) = make_uint2(pack16(o[0], o[1]), pack16(o[2], o[3]));
+        else *(int4*)((int32_t*)plain + e) = make_int4(o[0], o[1], o[2], o[3]);
+      }
     }
-  } else {
-#pragma unroll
-    for (int j = 0; j < 9; ++j) {
-      const int32_t z = (int32_t)(((int64_t)v[j] * U + 32768) >> 16);
-      o[j] = (int32_t)sat(rs((int64_t)z * g3[j], sh_out), bits_out);
-    }
-  }
-  if (planes) {   // K-blocked planes: element (row, lane + 64 j) at j M 64 + row 64 + lane
-    uint8_t* pb = planes + (size_t)row * 64 + lane;
-    const size_t pl = (size_t)M * kD, m64 = (size_t)M * 64;
-#pragma unroll
-    for (int j = 0; j < 9; ++j)
-#pragma unroll
-      for (int l = 0; l < OB; ++l) pb[l * pl + j * m64] = (uint8_t)limb_byte(o[j], l, OB);
-  }
-  if (plain) {
-#pragma unroll
-    for (int j = 0; j < 9; ++j) {
-      const size_t e = (size_t)row * kD + lane + 64 * j;
-      if constexpr (OB == 2) ((int16_t*)plain)[e] = (int16_t)o[j];
-      else ((int32_t*)plain)[e] = o[j];
-    }
-  }
+  };
+  if (sh_out >= 10 && sh_out <= 40) body(std::true_type{});
+  else body(std::false_type{});
 }
 
 // ------------------------------------------------------------------------------ rope
@@ -1191,7 +1198,7 @@ hipError_t embed(const int64_t* ids, int M, const int8_t* emb_q, const int32_t* 
 
 hipError_t rmsnorm(const int32_t* x, int M, const int32_t* gain, int sh_out, int bits_out, uint8_t* planes,
                    void* plain, hipStream_t s) {
-  dim3 grid((M + 3) / 4);
+  dim3 grid((M + 15) / 16);
   if (bits_out == 16) hipLaunchKernelGGL(rmsnorm_kernel<2>, grid, dim3(256), 0, s, x, M, gain, sh_out, bits_out, planes, plain);
   else hipLaunchKernelGGL(rmsnorm_kernel<4>, grid, dim3(256), 0, s, x, M, gain, sh_out, bits_out, planes, plain);
   return hipGetLastError();

@@ -139,7 +139,8 @@ int eii_linear(const void* A_dev, int a_bits, const int8_t* W_dev, const int32_t
                int out_bits, void* out_dev, void* stream);
 
 /* RMSNorm (python/intref.py:168-184): x_dev int32 [M, 576] -> out_dev [M, 576] of out_bits
- * (16 -> int16, 32 -> int32); gain_dev int32 [576] with exponent f_gain. */
+ * (16 -> int16, 32 -> int32); gain_dev int32 [576] with exponent f_gain; the three pointers
+ * 16-byte aligned. */
 int eii_rmsnorm(const int32_t* x_dev, int M, const int32_t* gain_dev, int f_gain, int f_out,
                 int out_bits, void* out_dev, void* stream);
 

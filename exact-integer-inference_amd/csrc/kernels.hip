@@ -339,7 +339,12 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
                   q = (int32_t)v;
                 }
               }
-              if (live(tm, e)) *at(tb, N, lane_b, tm, e, 32 * tn) = (OT)q;
+              if (live(tm, e)) {
+                // the logits (8 GB at 256 x 160 tokens) stream past the caches instead of evicting
+                // the operand tiles other workgroups are about to reuse
+                if constexpr (EPI == EPI_LOGITS) __builtin_nontemporal_store((OT)q, at(tb, N, lane_b, tm, e, 32 * tn));
+                else *at(tb, N, lane_b, tm, e, 32 * tn) = (OT)q;
+              }
             }
           }
         }

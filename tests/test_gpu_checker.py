@@ -81,3 +81,21 @@ def test_hash_and_manifest(vec):
 def test_reference_checker_accepts_gpu_vectors(vec):
     r = run([REF_BIN, str(vec / "t24")])
     assert r.returncode == 0 and "ALL STATES EXACT" in r.stdout, r.stdout[-2000:]
+
+
+def test_conformance_record(vec, tmp_path):
+    """python -m eii.conformance over the exported sets: hash check, the reference's C checker as
+    the CPU check (when built, for the set it can read: T <= 512), eii_check, the planted +1."""
+    from eii import conformance, export_vectors
+    assert export_vectors.hash_root(str(vec)) == 0
+    cpu = REF_BIN if os.path.exists(REF_BIN) else None
+    status, path = conformance.record(str(vec), str(tmp_path / "runs"), sets=["t24"], cpu_checker=cpu,
+                                      variants=(), timeout=240)
+    text = open(path).read()
+    print(text[-1500:])
+    assert status == 0, text
+    assert "negative test: detected" in text and "eii_check: pass" in text
+    assert f"exact lines: {2 if cpu else 1} ({2 if cpu else 1} expected" in text
+    status, path = conformance.record(str(vec), str(tmp_path / "runs2"), sets=["t24", "t600"], variants=(),
+                                      timeout=240)
+    assert status == 0, open(path).read()

@@ -381,7 +381,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
         const double sc = ldexp(1.0, -g.sh2), half = g.sh2 >= 1 ? ldexp(0.5, -g.sh2) : 0.0;
         const size_t pl = (size_t)g.M * (N / 2);
         uint8_t* tb = (uint8_t*)g.out + (size_t)nb * g.M * 64 + (size_t)m0 * 64;
-        const uint32_t lane_b = (uint32_t)rw * 64u + (uint32_t)(wn * 32 + fc);
+        const uint32_t lane_b4 = (uint32_t)(rw + (fc & 3)) * 64u + (uint32_t)(wn * 32 + (fc & ~3));
 #pragma unroll
         for (int tm = 0; tm < C::TM; ++tm) {
           int32_t gv[16], sv[16];
@@ -402,24 +402,46 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
             const int32_t t = *(const int32_t*)((const char*)g.aux_tab + (uint32_t)(inw[e] ? 32768 : gv[e] + 32768) * 4u);
             if (!inw[e]) sv[e] = t;
           }
+          int32_t vv[16];
 #pragma unroll
           for (int e = 0; e < 16; ++e) {
             // SAT(RS(silu * up, sh2), bits2): the product and the scaled sum are exact in float64
             const double x = (double)sv[e] * uv[e];
-            const int32_t v = rne_i32(fmin(fmax(fma(x, sc, half), lo), hi));
-            if (!live(tm, e)) continue;
-            uint8_t* ob = at(tb, 64, lane_b, tm, e, 0);
-            // limb bytes: the low bytes carry the -128 bias, the top byte is signed
-            if (g.bits2 == 16) {
-              const uint32_t vb = (uint32_t)v ^ 0x80u;
-              ob[0] = (uint8_t)vb;
-              ob[pl] = (uint8_t)(vb >> 8);
-            } else {
-              const uint32_t vb = (uint32_t)v ^ 0x808080u;
-              ob[0] = (uint8_t)vb;
-              ob[pl] = (uint8_t)(vb >> 8);
-              ob[2 * pl] = (uint8_t)(vb >> 16);
-              ob[3 * pl] = (uint8_t)(vb >> 24);
+            vv[e] = rne_i32(fmin(fmax(fma(x, sc, half), lo), hi));
+          }
+          // limb bytes (the low bytes carry the -128 bias, the top byte is signed) of rows
+          // r = 0..3 of each 4-row group, then a 4 x 4 byte transpose across the lanes of a quad:
+          // lane j of the quad ends with row j, columns 4 (fc / 4) .. + 3, one dword per plane
+          const uint32_t xb = g.bits2 == 16 ? 0x80u : 0x808080u;
+          const uint32_t sel1 = (lane & 1) ? 0x03070105u : 0x06020400u;
+          const uint32_t sel2 = (lane & 2) ? 0x03020706u : 0x05040100u;
+          auto tr4 = [&](uint32_t w) __attribute__((always_inline)) {
+            uint32_t x = (uint32_t)__builtin_amdgcn_mov_dpp((int)w, 0xB1, 0xF, 0xF, false);
+            w = __builtin_amdgcn_perm(x, w, sel1);
+            x = (uint32_t)__builtin_amdgcn_mov_dpp((int)w, 0x4E, 0xF, 0xF, false);
+            return __builtin_amdgcn_perm(x, w, sel2);
+          };
+#pragma unroll
+          for (int b = 0; b < 4; ++b) {
+            const uint32_t v0 = (uint32_t)vv[4 * b] ^ xb, v1 = (uint32_t)vv[4 * b + 1] ^ xb;
+            const uint32_t v2 = (uint32_t)vv[4 * b + 2] ^ xb, v3 = (uint32_t)vv[4 * b + 3] ^ xb;
+            const uint32_t t01 = __builtin_amdgcn_perm(v1, v0, 0x05010400u), t23 = __builtin_amdgcn_perm(v3, v2, 0x05010400u);
+            const uint32_t p0 = tr4(__builtin_amdgcn_perm(t23, t01, 0x05040100u));
+            const uint32_t p1 = tr4(__builtin_amdgcn_perm(t23, t01, 0x07060302u));
+            uint32_t p2 = 0, p3 = 0;
+            if (g.bits2 != 16) {
+              const uint32_t u01 = __builtin_amdgcn_perm(v1, v0, 0x07030602u), u23 = __builtin_amdgcn_perm(v3, v2, 0x07030602u);
+              p2 = tr4(__builtin_amdgcn_perm(u23, u01, 0x05040100u));
+              p3 = tr4(__builtin_amdgcn_perm(u23, u01, 0x07060302u));
+            }
+            const int row = 32 * tm + 8 * b;   // + the lane's rw + (fc & 3)
+            if (!full && m0 + rw + (fc & 3) + row >= g.M) continue;
+            uint32_t* ob = (uint32_t*)(tb + (size_t)row * 64 + lane_b4);
+            ob[0] = p0;
+            *(uint32_t*)((uint8_t*)ob + pl) = p1;
+            if (g.bits2 != 16) {
+              *(uint32_t*)((uint8_t*)ob + 2 * pl) = p2;
+              *(uint32_t*)((uint8_t*)ob + 3 * pl) = p3;
             }
           }
         }

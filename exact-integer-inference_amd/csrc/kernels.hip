@@ -34,11 +34,12 @@ __device__ __forceinline__ int lds_swz(int row, int c) { return c ^ ((row >> 2) 
 constexpr int vmcnt_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
 
 // Limb planes of 4 int16 values packed in two dwords: (low bytes - 128, high bytes).
+// (v_perm_b32 byte i = byte sel[i] of the 8 bytes d1:d0, d0 being bytes 0..3)
 __device__ __forceinline__ uint32_t lo_bytes16(uint32_t d0, uint32_t d1) {
-  return ((d0 & 0xFFu) | ((d0 >> 8) & 0xFF00u) | ((d1 << 16) & 0xFF0000u) | ((d1 << 8) & 0xFF000000u)) ^ 0x80808080u;
+  return __builtin_amdgcn_perm(d1, d0, 0x06040200u) ^ 0x80808080u;
 }
 __device__ __forceinline__ uint32_t hi_bytes16(uint32_t d0, uint32_t d1) {
-  return ((d0 >> 8) & 0xFFu) | ((d0 >> 16) & 0xFF00u) | ((d1 << 8) & 0xFF0000u) | (d1 & 0xFF000000u);
+  return __builtin_amdgcn_perm(d1, d0, 0x07050301u);
 }
 // Limb byte l of a W-byte activation v (eii_int.h split_limbs): low bytes biased by -128, the top
 // byte signed.
@@ -843,8 +844,7 @@ __global__ __launch_bounds__(256) void silu_kernel(const int16_t* gu, int M, con
 // exp-sum and probability passes; NKT == 0: every pass recomputes the scores (long sequences).
 constexpr int32_t kMasked = -32768;   // no score exceeds it, so the row max never picks it
 
-__device__ __forceinline__ int32_t sum16x8(u32x4 d) {   // sum of the 8 int16 values in d
-  int32_t s = 0;
+__device__ __forceinline__ int32_t sum16x8(u32x4 d, int32_t s = 0) {   // s + the 8 int16 values in d
 #pragma unroll
   for (int i = 0; i < 4; ++i) s += ((int32_t)(d[i] << 16) >> 16) + ((int32_t)d[i] >> 16);
   return s;
@@ -882,7 +882,7 @@ __global__ __launch_bounds__(192) __attribute__((amdgpu_waves_per_eu(2))) void a
                   (int)lo_bytes16(d1[2], d1[3])};
       qh[s] = v4i{(int)hi_bytes16(d0[0], d0[1]), (int)hi_bytes16(d0[2], d0[3]), (int)hi_bytes16(d1[0], d1[1]),
                   (int)hi_bytes16(d1[2], d1[3])};
-      sum += sum16x8(d0) + sum16x8(d1);
+      sum = sum16x8(d1, sum16x8(d0, sum));
     }
     sum += __shfl_xor(sum, 32);
     cq = 128 * sum - (1 << 20) + (1 << (sh - 1));   // with the rounding offset of RS(., sh)
@@ -911,7 +911,7 @@ __global__ __launch_bounds__(192) __attribute__((amdgpu_waves_per_eu(2))) void a
                   (int)lo_bytes16(d1[2], d1[3])};
       kh[s] = v4i{(int)hi_bytes16(d0[0], d0[1]), (int)hi_bytes16(d0[2], d0[3]), (int)hi_bytes16(d1[0], d1[1]),
                   (int)hi_bytes16(d1[2], d1[3])};
-      ks += sum16x8(d0) + sum16x8(d1);
+      ks = sum16x8(d1, sum16x8(d0, ks));
     }
     ks += __shfl_xor(ks, 32);
     skl[w][pic] = 128 * ks;   // lanes c and c + 32 store the same value
@@ -964,14 +964,16 @@ __global__ __launch_bounds__(192) __attribute__((amdgpu_waves_per_eu(2))) void a
 #pragma unroll
   for (int i = 0; i < 2; ++i) C16[i] = C8[i] = C0[i] = v16i{};
   int32_t SP = 0;
-  double Zd = 0.0, rZ = 0.0, Zh = 0.0;
+  double Zs = 0.0, rZs = 0.0, Zhs = 0.0;   // Z 2^-16, RN(2^16 / Z), floor(Z / 2) 2^-16
   // P = floor((e 65536 + floor(Z / 2)) / Z) (python/intref.py:245-246).  num / Z <= 65536.5 (e is
   // a term of Z), and num rZ + 2^-30 evaluated with one fma is within 2^-36 of num / Z + 2^-30, so
   // its floor is the true quotient or one more; the exact float64 remainder takes the one back.
+  // Everything runs scaled by 2^-16 (num 2^-16 = e + floor(Z / 2) 2^-16 is one exact add), which
+  // changes no rounding: the scaled quotient estimate and remainder are the unscaled ones exactly.
   auto prob = [&](int32_t e) __attribute__((always_inline)) -> int32_t {
-    const double num = fma((double)e, 65536.0, Zh);
-    const double q = floor(fma(num, rZ, 0x1p-30));
-    const double rem = fma(-q, Zd, num);
+    const double num = (double)e + Zhs;
+    const double q = floor(fma(num, rZs, 0x1p-30));
+    const double rem = fma(-q, Zs, num);
     return (int32_t)q - (rem < 0.0 ? 1 : 0);
   };
   // probabilities of key tile g (e values) into limb operands, then the P.V MFMAs.  R1 =
@@ -990,23 +992,30 @@ __global__ __launch_bounds__(192) __attribute__((amdgpu_waves_per_eu(2))) void a
     }
   };
   auto pv = [&](const VFrag& vf, const int32_t (&ev)[16]) __attribute__((always_inline)) {
-    uint32_t w0[4], w1[4];
-    int32_t rest[16];
-    int32_t anyrest = 0;
+    // byte r of a word = element 4 i + r
+    auto bytes4 = [](const int32_t (&v)[4]) __attribute__((always_inline)) {
+      return __builtin_amdgcn_perm(__builtin_amdgcn_perm(v[3], v[2], 0x0c0c0400u),
+                                   __builtin_amdgcn_perm(v[1], v[0], 0x0c0c0400u), 0x05040100u);
+    };
+    uint32_t w0[4], w1[4], wb[4], wc[4];
+    int32_t rmax = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      uint32_t b0 = 0, b1 = 0;
+      int32_t P[4], p1[4], pb[4], pc[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int32_t P = prob(ev[4 * i + r]);
-        SP += P;
-        const int32_t R1 = (P + 128) >> 8, p1 = min(R1, 127);
-        rest[4 * i + r] = R1 - p1;
-        anyrest |= R1 - p1;
-        b0 |= ((uint32_t)P & 0xFFu) << (8 * r);
-        b1 |= (uint32_t)p1 << (8 * r);
+        P[r] = prob(ev[4 * i + r]);
+        const int32_t R1 = (P[r] + 128) >> 8;
+        rmax = max(rmax, R1);
+        p1[r] = min(R1, 127);
+        pb[r] = min(R1 - p1[r], 127);
+        pc[r] = R1 - p1[r] - pb[r];
       }
-      w0[i] = b0; w1[i] = b1;
+      SP += (P[0] + P[1]) + (P[2] + P[3]);
+      w0[i] = bytes4(P);    // low bytes of P
+      w1[i] = bytes4(p1);
+      wb[i] = bytes4(pb);
+      wc[i] = bytes4(pc);
     }
     const v4i P0 = v4i{(int)w0[0], (int)w0[1], (int)w0[2], (int)w0[3]};
     const v4i P1 = v4i{(int)w1[0], (int)w1[1], (int)w1[2], (int)w1[3]};
@@ -1019,24 +1028,10 @@ __global__ __launch_bounds__(192) __attribute__((amdgpu_waves_per_eu(2))) void a
       C8[dt] = mfma32(VL[dt], P1, C8[dt]);
       C0[dt] = mfma32(VL[dt], P0, C0[dt]);
     }
-    if (__any(anyrest != 0)) {
-      uint32_t wb[4], wc[4];
-      int32_t anyc = 0;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        uint32_t bb = 0, bc = 0;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int32_t rb = min(rest[4 * i + r], 127), rc = rest[4 * i + r] - rb;
-          anyc |= rc;
-          bb |= (uint32_t)rb << (8 * r);
-          bc |= (uint32_t)rc << (8 * r);
-        }
-        wb[i] = bb; wc[i] = bc;
-      }
+    if (__any(rmax > 127)) {
       const v4i P1b = v4i{(int)wb[0], (int)wb[1], (int)wb[2], (int)wb[3]};
       const v4i P1c = v4i{(int)wc[0], (int)wc[1], (int)wc[2], (int)wc[3]};
-      const bool three = __any(anyc != 0);
+      const bool three = __any(rmax > 254);
 #pragma unroll
       for (int dt = 0; dt < 2; ++dt) {
         C16[dt] = mfma32(VH[dt], P1b, C16[dt]);
@@ -1050,9 +1045,10 @@ __global__ __launch_bounds__(192) __attribute__((amdgpu_waves_per_eu(2))) void a
   };
   auto set_z = [&](int64_t Z) __attribute__((always_inline)) {
     Z += __shfl_xor(Z, 32);
-    Zd = (double)Z;
-    rZ = 1.0 / Zd;
-    Zh = (double)(Z >> 1);
+    const double Zd = (double)Z;   // Z < 2^43: exact
+    Zs = Zd * 0x1p-16;
+    rZs = (1.0 / Zd) * 65536.0;
+    Zhs = (double)(Z >> 1) * 0x1p-16;
   };
 
   int32_t rowmax = kMasked;
@@ -1060,54 +1056,9 @@ __global__ __launch_bounds__(192) __attribute__((amdgpu_waves_per_eu(2))) void a
   constexpr bool ahead = NKT > 0 && NKT <= 5;
   KRows kr[ahead ? 2 : 1];
   VFrag vf[ahead ? 2 : 1];
-  if constexpr (NKT > 0) {
-    uint32_t pk[NKT][8];   // packed int16 scores
-    if constexpr (ahead) load_k(g0, kr[0]);
-#pragma unroll
-    for (int t = 0; t < NKT; ++t) {
-      if (t < ntile) {
-        if constexpr (ahead) {
-          if (t + 1 < ntile) load_k(g0 + t + 1, kr[(t + 1) & 1]);
-          else load_v(g0, vf[0]);   // the first V tile, while the last scores and the sums run
-        } else {
-          load_k(g0 + t, kr[0]);
-        }
-        int32_t sc[16];
-        scores(g0 + t, kr[ahead ? t & 1 : 0], sc);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          pk[t][i] = ((uint32_t)sc[2 * i] & 0xFFFFu) | ((uint32_t)sc[2 * i + 1] << 16);
-          rowmax = max(rowmax, max(sc[2 * i], sc[2 * i + 1]));
-        }
-      }
-    }
-    rowmax = max(rowmax, __shfl_xor(rowmax, 32));
-    auto unpack = [&](int t, int j) __attribute__((always_inline)) -> int32_t {
-      const uint32_t p = pk[t][j >> 1];
-      return (j & 1) ? (int32_t)p >> 16 : (int32_t)(p << 16) >> 16;
-    };
-    int64_t Z = 0;
-#pragma unroll
-    for (int t = 0; t < NKT; ++t)
-      if (t < ntile) {
-#pragma unroll
-        for (int j = 0; j < 16; ++j) Z += expo(g0 + t, j, unpack(t, j), rowmax);
-      }
-    set_z(Z);
-#pragma unroll
-    for (int t = 0; t < NKT; ++t)
-      if (t < ntile) {
-        if constexpr (ahead) {
-          if (t + 1 < ntile) load_v(g0 + t + 1, vf[(t + 1) & 1]);
-        } else {
-          load_v(g0 + t, vf[0]);
-        }
-        int32_t ev[16];
-#pragma unroll
-        for (int j = 0; j < 16; ++j) ev[j] = expo(g0 + t, j, unpack(t, j), rowmax);
-        pv(vf[ahead ? t & 1 : 0], ev);
-      }
-  } else {
+  // every pass recomputes the scores and tests the keys
+  auto recompute_passes = [&]() __attribute__((always_inline)) {
+    rowmax = kMasked;
 #pragma unroll 1
     for (int t = 0; t < ntile; ++t) {
       int32_t sc[16];
@@ -1137,6 +1088,83 @@ __global__ __launch_bounds__(192) __attribute__((amdgpu_waves_per_eu(2))) void a
       for (int j = 0; j < 16; ++j) sc[j] = expo(g0 + t, j, sc[j], rowmax);
       pv(vf[0], sc);
     }
+  };
+  if constexpr (NKT > 0) {
+    uint32_t pk[NKT][8];   // packed int16 scores
+    if constexpr (ahead) load_k(g0, kr[0]);
+#pragma unroll
+    for (int t = 0; t < NKT; ++t) {
+      if (t < ntile) {
+        if constexpr (ahead) {
+          if (t + 1 < ntile) load_k(g0 + t + 1, kr[(t + 1) & 1]);
+          else load_v(g0, vf[0]);   // the first V tile, while the last scores and the sums run
+        } else {
+          load_k(g0 + t, kr[0]);
+        }
+        int32_t sc[16];
+        scores(g0 + t, kr[ahead ? t & 1 : 0], sc);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          pk[t][i] = ((uint32_t)sc[2 * i] & 0xFFFFu) | ((uint32_t)sc[2 * i + 1] << 16);
+          rowmax = max(rowmax, max(sc[2 * i], sc[2 * i + 1]));
+        }
+      }
+    }
+    rowmax = max(rowmax, __shfl_xor(rowmax, 32));
+    auto unpack = [&](int t, int j) __attribute__((always_inline)) -> int32_t {
+      const uint32_t p = pk[t][j >> 1];
+      return (j & 1) ? (int32_t)p >> 16 : (int32_t)(p << 16) >> 16;
+    };
+    // e = E[min(rowmax - s, 1537)] directly, with no key tests: a masked key holds score kMasked,
+    // which lies more than 1536 below the row max (table entry 1537 = 0) whenever the row max
+    // exceeds kMasked + 1536.  In waves with a row whose every score is near -32768, the tiles
+    // holding keys outside [sequence start, query] (the diagonal tile, and the first one when the
+    // sequence does not start on a 32-row boundary) test the keys; the branch is uniform per tile.
+    const bool clean = __all(rowmax > kMasked + kDMax);
+    auto edge = [&](int t) __attribute__((always_inline)) {
+      return !clean && (32 * (g0 + t) < s0 || 32 * (g0 + t) + 31 > q0);
+    };
+    auto ex = [&](int t, int j) __attribute__((always_inline)) -> int32_t {
+      return etab[min(rowmax - unpack(t, j), kDMax + 1)];
+    };
+    // Z: e <= 2^30, so sums of three fit uint32
+    uint64_t Z = 0;
+#pragma unroll
+    for (int t = 0; t < NKT; ++t)
+      if (t < ntile) {
+        uint32_t ev[16];
+        if (edge(t)) {
+#pragma unroll
+          for (int j = 0; j < 16; ++j) ev[j] = expo(g0 + t, j, unpack(t, j), rowmax);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 16; ++j) ev[j] = ex(t, j);
+        }
+#pragma unroll
+        for (int j = 0; j < 15; j += 3) Z += ev[j] + ev[j + 1] + ev[j + 2];
+        Z += ev[15];
+      }
+    set_z((int64_t)Z);
+#pragma unroll
+    for (int t = 0; t < NKT; ++t)
+      if (t < ntile) {
+        if constexpr (ahead) {
+          if (t + 1 < ntile) load_v(g0 + t + 1, vf[(t + 1) & 1]);
+        } else {
+          load_v(g0 + t, vf[0]);
+        }
+        int32_t ev[16];
+        if (edge(t)) {
+#pragma unroll
+          for (int j = 0; j < 16; ++j) ev[j] = expo(g0 + t, j, unpack(t, j), rowmax);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 16; ++j) ev[j] = ex(t, j);
+        }
+        pv(vf[ahead ? t & 1 : 0], ev);
+      }
+  } else {
+    recompute_passes();
   }
   SP += __shfl_xor(SP, 32);
 

@@ -85,11 +85,14 @@ def test_rmsnorm(oracle):
         np.testing.assert_array_equal(out.cpu().numpy().astype(np.int64), want)
 
 
-def _attention_case(oracle, lens, scale, seed, f_qr=10, f_kr=9, f_v=11, f_c=11, bits_c=16):
+def _attention_case(oracle, lens, scale, seed, f_qr=10, f_kr=9, f_v=11, f_c=11, bits_c=16, floor=False):
     lib = L.load()
     rng = np.random.default_rng(seed)
     M = sum(lens)
     qkv = np.clip(np.round(rng.standard_normal((M, 960)) * scale), -32768, 32767).astype(np.int16)
+    if floor:   # q >= 0 and k <= 0: every q.k is far below zero
+        qkv[:, :576] = np.minimum(np.abs(qkv[:, :576].astype(np.int64)), 32767)
+        qkv[:, 576:768] = -np.minimum(np.abs(qkv[:, 576:768].astype(np.int64)), 32767)
     off = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
     E = exp_table().astype(np.int32)
     ctx = torch.empty((M, 576), dtype=torch.int16 if bits_c == 16 else torch.int32, device="cuda")
@@ -117,6 +120,13 @@ def test_attention_spread(oracle, lens, scale):
 def test_attention_saturated(oracle):
     # scores pinned at the 16-bit limits: many keys fall beyond the table (d > 1536), P = 65536 occurs
     _attention_case(oracle, [150, 7], scale=20000.0, seed=3, f_qr=8, f_kr=8)
+
+
+@pytest.mark.parametrize("lens", [[150, 7], [33, 200], [64, 96]])
+def test_attention_scores_at_floor(oracle, lens):
+    # every score saturates at -32768: the row max is -32768, so a masked key (score -32768) would
+    # fall inside the exp table; the tiles holding masked keys must test them
+    _attention_case(oracle, lens, scale=20000.0, seed=11 + len(lens), f_qr=8, f_kr=8, floor=True)
 
 
 def test_attention_ctx32(oracle):

@@ -1056,7 +1056,8 @@ __global__ __launch_bounds__(192) __attribute__((amdgpu_waves_per_eu(2))) void a
   constexpr bool ahead = NKT > 0 && NKT <= 5;
   KRows kr[ahead ? 2 : 1];
   VFrag vf[ahead ? 2 : 1];
-  // every pass recomputes the scores and tests the keys
+  // every pass recomputes the scores; the exp lookups test keys only in waves with a row max
+  // near -32768 (see the register-resident passes below)
   auto recompute_passes = [&]() __attribute__((always_inline)) {
     rowmax = kMasked;
 #pragma unroll 1
@@ -1068,26 +1069,35 @@ __global__ __launch_bounds__(192) __attribute__((amdgpu_waves_per_eu(2))) void a
       for (int j = 0; j < 16; ++j) rowmax = max(rowmax, sc[j]);
     }
     rowmax = max(rowmax, __shfl_xor(rowmax, 32));
-    int64_t Z = 0;
+    auto passes = [&](auto CLEAN) __attribute__((always_inline)) {
+      auto ex = [&](int t, int j, int32_t s) __attribute__((always_inline)) -> uint32_t {
+        if constexpr (decltype(CLEAN)::value) return (uint32_t)etab[min(rowmax - s, kDMax + 1)];
+        else return (uint32_t)expo(g0 + t, j, s, rowmax);
+      };
+      uint64_t Z = 0;   // e <= 2^30: sums of three fit uint32
 #pragma unroll 1
-    for (int t = 0; t < ntile; ++t) {
-      int32_t sc[16];
-      load_k(g0 + t, kr[0]);
-      scores(g0 + t, kr[0], sc);
+      for (int t = 0; t < ntile; ++t) {
+        int32_t sc[16];
+        load_k(g0 + t, kr[0]);
+        scores(g0 + t, kr[0], sc);
 #pragma unroll
-      for (int j = 0; j < 16; ++j) Z += expo(g0 + t, j, sc[j], rowmax);
-    }
-    set_z(Z);
+        for (int j = 0; j < 15; j += 3) Z += ex(t, j, sc[j]) + ex(t, j + 1, sc[j + 1]) + ex(t, j + 2, sc[j + 2]);
+        Z += ex(t, 15, sc[15]);
+      }
+      set_z((int64_t)Z);
 #pragma unroll 1
-    for (int t = 0; t < ntile; ++t) {
-      int32_t sc[16];
-      load_k(g0 + t, kr[0]);
-      load_v(g0 + t, vf[0]);
-      scores(g0 + t, kr[0], sc);
+      for (int t = 0; t < ntile; ++t) {
+        int32_t sc[16];
+        load_k(g0 + t, kr[0]);
+        load_v(g0 + t, vf[0]);
+        scores(g0 + t, kr[0], sc);
 #pragma unroll
-      for (int j = 0; j < 16; ++j) sc[j] = expo(g0 + t, j, sc[j], rowmax);
-      pv(vf[0], sc);
-    }
+        for (int j = 0; j < 16; ++j) sc[j] = (int32_t)ex(t, j, sc[j]);
+        pv(vf[0], sc);
+      }
+    };
+    if (__all(rowmax > kMasked + kDMax)) passes(std::true_type{});
+    else passes(std::false_type{});
   };
   if constexpr (NKT > 0) {
     uint32_t pk[NKT][8];   // packed int16 scores

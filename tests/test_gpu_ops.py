@@ -122,7 +122,7 @@ def test_attention_saturated(oracle):
     _attention_case(oracle, [150, 7], scale=20000.0, seed=3, f_qr=8, f_kr=8)
 
 
-@pytest.mark.parametrize("lens", [[150, 7], [33, 200], [64, 96]])
+@pytest.mark.parametrize("lens", [[150, 7], [33, 200], [64, 96], [45, 300]])
 def test_attention_scores_at_floor(oracle, lens):
     # every score saturates at -32768: the row max is -32768, so a masked key (score -32768) would
     # fall inside the exp table; the tiles holding masked keys must test them

@@ -56,7 +56,7 @@ __device__ __forceinline__ uint32_t limb_word(const int32_t* v, int l, int W) {
 // ------------------------------------------------------------------------------ GEMM
 // Persistent workgroups of 4 waves, two per CU, sweep BM x BN output tiles (128 x 128 for 2-limb
 // activations, 64 x 128 for 4-limb, 64 x 192 for 2-limb residual GEMMs with N = 576) in a flat
-// (tile, K block of 64) loop.  Activation limb planes go global -> LDS through 4-8 stages;
+// (tile, K block of 64) loop.  Activation limb planes go global -> LDS through 4 stages;
 // each wave loads its weight fragments straight into registers (the weights are L2-resident)
 // two steps ahead.  v_mfma_i32_32x32x32_i8 sustains about twice the int8 rate of the 16x16x64
 // form on gfx950.

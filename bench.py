@@ -122,6 +122,43 @@ def cpu_baseline_port(model_path, ids):
             "sample": f"1 sequence x {T} tokens, numpy oracle (float64 BLAS exact products)", "seconds": s}
 
 
+def decode_bench(args):
+    """KV-cached decoding over the configuration's batch: prompt = the first T - steps tokens,
+    then steps appends of one token per sequence (the next token of the synthetic ids, so the
+    logits equal those of the full forward), the last steps - warmup of them timed."""
+    import torch
+    from eii import synth
+    from eii.engine import Engine
+    ids_np = synth.token_ids(args.config)
+    B, T = ids_np.shape
+    n = args.steps
+    if not 0 < args.warmup < n < T:
+        raise SystemExit("--decode needs 0 < --warmup < --steps < tokens per sequence")
+    eng = Engine(synth.ensure_model("stress" if args.config == "cfg5" else "base"), rope_rows=max(512, T))
+    ids = torch.from_numpy(ids_np).cuda()
+    kv = eng.kv_cache(B, T)
+    try:
+        kv.append(ids[:, :T - n], logits=False)
+        for t in range(T - n, T - n + args.warmup):
+            kv.append(ids[:, t:t + 1])
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for t in range(T - n + args.warmup, T):
+            kv.append(ids[:, t:t + 1], check=False)
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+        eng.check()
+    finally:
+        kv.close()
+    steps = n - args.warmup
+    print(json.dumps({"metric": "KV-cached decode tokens/s (one new token per sequence per step)",
+                      "value": B * steps / elapsed, "unit": "tokens/s", "n_gpus": 1, "steps": steps,
+                      "warmup": args.warmup, "ms_per_step": elapsed * 1e3 / steps, "higher_is_better": True,
+                      "dtype": "int8", "data": "synthetic",
+                      "config": {"workload": f"{args.config}: {B} sequences, {T - n}-token prompt, then single-token "
+                                             f"appends with int32 logits [{B}, 1, {V}]", "batch": B}}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -131,9 +168,15 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy (the byte-counter calibration) and exit")
+    ap.add_argument("--decode", action="store_true",
+                    help="time KV-cached decoding instead: the configuration's sequences minus their last "
+                         "--steps tokens as the prompt, then --steps single-token appends (one JSON line)")
     args = ap.parse_args()
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.decode:
+        decode_bench(args)
         return
     if args.gpus != 1:
         print(f"bench.py: this engine runs on one GPU (sequences shard across GPUs with no exchange, "

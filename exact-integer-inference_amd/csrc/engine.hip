@@ -975,6 +975,8 @@ extern "C" int eii_attention(const int16_t* qkv, const int32_t* seq_off, int nse
   const int shift_s = f_qr + f_kr + 3 - kFScore;
   if (shift_s < 1) return fail(EII_E_BOUND, "score shift < 1");
   if (shift_s > 30) return fail(EII_E_BOUND, "score shift > 30");
+  int rc = check_scalar_shift(16 + f_v - f_c, "context");
+  if (rc) return rc;
   if (max_T > 16384) return fail(EII_E_BOUND, "sequences longer than 16384 tokens are not supported");
   hipStream_t s = (hipStream_t)stream;
   // the row offsets decide the launch shape: read them back

@@ -891,8 +891,9 @@ __global__ __launch_bounds__(192) __attribute__((amdgpu_waves_per_eu(2))) void a
   // K rows of key tile g for this lane (row pi(c) of the tile, d = 32 s + 16 h + 0..15), loaded
   // one tile ahead of their use
   struct KRows { u32x4 d[2][2]; };
+  const int16_t* const kbase = a.qkv + kD + kvg * 64 + 16 * h;   // row offsets below 2^31 elements
   auto load_k = [&](int g, KRows& kr) __attribute__((always_inline)) {
-    const int16_t* kp = a.qkv + (size_t)min(32 * g + pic, a.M - 1) * kQKVN + kD + kvg * 64 + 16 * h;
+    const int16_t* kp = kbase + (uint32_t)min(32 * g + pic, a.M - 1) * (uint32_t)kQKVN;
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       kr.d[s][0] = *(const u32x4*)(kp + 32 * s);
@@ -982,11 +983,12 @@ __global__ __launch_bounds__(192) __attribute__((amdgpu_waves_per_eu(2))) void a
   // P1c = R1 - P1 - P1b, all with the weight of P1.
   // V^T limb fragments of key tile g (A operands of the two 32-row d tiles), loaded one tile ahead
   struct VFrag { v4i L[2], H[2]; };
+  const size_t vpl = (size_t)192 * vts;
+  const uint8_t* const vbase = a.vt + (size_t)(kvg * 64 + c) * vts + 16 * h;
   auto load_v = [&](int g, VFrag& vf) __attribute__((always_inline)) {
-    const size_t vpl = (size_t)192 * vts;
 #pragma unroll
     for (int dt = 0; dt < 2; ++dt) {
-      const uint8_t* vp = a.vt + (size_t)(kvg * 64 + 32 * dt + c) * vts + 32 * g + 16 * h;
+      const uint8_t* vp = vbase + (size_t)(32 * dt) * vts + (uint32_t)(32 * g);
       vf.L[dt] = *(const v4i*)vp;
       vf.H[dt] = *(const v4i*)(vp + vpl);
     }
@@ -1183,6 +1185,11 @@ __global__ __launch_bounds__(192) __attribute__((amdgpu_waves_per_eu(2))) void a
   const int outM = a.kv_len ? a.out_M : a.M;
   const int qo = a.kv_len ? seq * (T - a.q_first) + qi - s0 - a.q_first : qi;   // output row
   const size_t orow = (size_t)qo * kD + hh * 64, pl = (size_t)outM * kD;
+  // SAT(RS(acc, sh_ctx), bits_c) in float64, where every step is exact for the shifts the callers
+  // admit (-30 .. 62): |C16| <= T 256 128 <= 2^29, so |acc| < 2^47; acc 2^-sh + 1/2 is exact
+  // whenever its floor can differ from 0 or from a value past the saturation bounds
+  const double sp128 = 128.0 * (double)SP, sc = ldexp(1.0, -a.sh_ctx);
+  const double clo = -ldexp(1.0, a.bits_c - 1), chi = ldexp(1.0, a.bits_c - 1) - 1.0;
 #pragma unroll
   for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
@@ -1191,8 +1198,8 @@ __global__ __launch_bounds__(192) __attribute__((amdgpu_waves_per_eu(2))) void a
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int j = 4 * b + r;
-        const int64_t acc = (int64_t)C16[dt][j] * 65536 + (int64_t)C8[dt][j] * 256 + C0[dt][j] + 128 * (int64_t)SP;
-        cv[r] = (int32_t)sat(rs(acc, a.sh_ctx), a.bits_c);
+        const double acc = fma((double)C16[dt][j], 65536.0, fma((double)C8[dt][j], 256.0, (double)C0[dt][j] + sp128));
+        cv[r] = (int32_t)fmin(fmax(floor(fma(acc, sc, 0.5)), clo), chi);
       }
       const int d0 = 32 * dt + 8 * b + 4 * h;
       if (a.ctx_planes) {

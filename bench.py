@@ -122,6 +122,53 @@ def cpu_baseline_port(model_path, ids):
             "sample": f"1 sequence x {T} tokens, numpy oracle (float64 BLAS exact products)", "seconds": s}
 
 
+def gemm_sweep(args):
+    """The exact-matmul sweep (eii_gemm_i8: int64 A W^T) at the projection shapes with 4096 rows of
+    int32 and int16 activations; one JSON line with a record per shape and width.  Time = the
+    whole operator (limb split of A, fragment order of W, the GEMM) per call, from events around
+    --steps calls after --warmup.  Roofline: the int8 MFMA peak divided by the limb count, and
+    8 TB/s over the algorithmic bytes (A, W, int64 output)."""
+    import torch
+    from eii import synth
+    from eii import lib as L
+    lib = L.load()
+    recs = []
+    for a_bits in (32, 16):
+        for K, N in synth.GEMM_SHAPES:
+            A, W = synth.gemm_inputs(K, N, a_bits)
+            M = A.shape[0]
+            At, Wt = torch.from_numpy(A).cuda(), torch.from_numpy(W).cuda()
+            acc = torch.empty((M, N), dtype=torch.int64, device="cuda")
+            wsum = torch.empty(N, dtype=torch.int32, device="cuda")
+            L.check(lib.eii_weight_colsum(Wt.data_ptr(), N, K, wsum.data_ptr(), None))
+
+            def call():
+                L.check(lib.eii_gemm_i8_ws(At.data_ptr(), a_bits, Wt.data_ptr(), wsum.data_ptr(), M, N, K,
+                                           acc.data_ptr(), None))
+            for _ in range(args.warmup):
+                call()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            e0.record()
+            for _ in range(args.steps):
+                call()
+            e1.record()
+            torch.cuda.synchronize()
+            t = e0.elapsed_time(e1) * 1e-3 / args.steps
+            limbs = a_bits // 8
+            ops = 2.0 * M * N * K
+            nbytes = (a_bits // 8) * M * K + N * K + 8 * M * N
+            t_mfma, t_hbm = ops * limbs / 5.0e15, nbytes / 8.0e12
+            recs.append({"K": K, "N": N, "a_bits": a_bits, "us": t * 1e6, "tops": ops / t / 1e12,
+                         "gb_s": nbytes / t / 1e9, "mfma_frac": t_mfma / t, "hbm_frac": t_hbm / t,
+                         "attainable_frac": max(t_mfma, t_hbm) / t, "bound": "mfma" if t_mfma > t_hbm else "hbm"})
+            del At, Wt, acc
+    print(json.dumps({"metric": "exact int64 matmul A W^T, 4096 rows (operator time incl. limb split)",
+                      "unit": "per-shape records", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+                      "dtype": "int8", "data": "synthetic", "config": {"workload": "cfg2: (K, N) projection shapes",
+                      "rows": synth.GEMM_M}, "results": recs}), flush=True)
+
+
 def decode_bench(args):
     """KV-cached decoding over the configuration's batch: prompt = the first T - steps tokens,
     then steps appends of one token per sequence (the next token of the synthetic ids, so the
@@ -177,6 +224,9 @@ def main():
         return
     if args.decode:
         decode_bench(args)
+        return
+    if args.config == "cfg2":
+        gemm_sweep(args)
         return
     if args.gpus != 1:
         print(f"bench.py: this engine runs on one GPU (sequences shard across GPUs with no exchange, "

@@ -305,7 +305,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
           if constexpr (EPI == EPI_I64) {
 #pragma unroll
             for (int e = 0; e < 16; ++e)
-              if (live(tm, e)) *at(tb, N, lane_b, tm, e, 32 * tn) = acc64(tm, tn, e, ws);
+              if (live(tm, e)) __builtin_nontemporal_store(acc64(tm, tn, e, ws), at(tb, N, lane_b, tm, e, 32 * tn));
             continue;
           }
           // residual epilogue: the loads of 8 rows issue together, then their updates

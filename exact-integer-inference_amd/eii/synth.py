@@ -35,7 +35,24 @@ CONFIGS = {
 CFG4_SAMPLED = (0, 37, 74, 111, 148, 185, 222, 255)
 CFG5_SAMPLED = (0, 31)
 
-GEMM_SHAPES = ((576, 576), (576, 192), (576, 1536), (1536, 576), (576, 49152))
+GEMM_SHAPES = ((576, 576), (576, 192), (576, 1536), (1536, 576), (576, 49152))   # (K, N)
+GEMM_M = 4096
+
+
+def gemm_inputs(K, N, a_bits, M=GEMM_M):
+    """The exact-matmul sweep's operands (python/intref.py:58-63 at the projection shapes): A [M, K]
+    int16 or int32 with 99 % of the entries uniform in [-2^10, 2^10] and 1 % uniform over the
+    whole type, the two extremes included; W int8 [N, K] uniform in [-127, 127].  Seeded by
+    (K, N, a_bits)."""
+    rng = np.random.default_rng([K, N, a_bits])
+    dt = np.int16 if a_bits == 16 else np.int32
+    info = np.iinfo(dt)
+    A = rng.integers(-2 ** 10, 2 ** 10, size=(M, K), endpoint=True, dtype=np.int64)
+    wide = rng.random((M, K)) < 0.01
+    A[wide] = rng.integers(info.min, info.max, size=int(wide.sum()), endpoint=True, dtype=np.int64)
+    A[0, 0], A[0, 1], A[M - 1, K - 1] = info.min, info.max, info.min
+    W = rng.integers(-127, 128, size=(N, K), dtype=np.int8)
+    return A.astype(dt), W
 
 
 def token_ids(cfg):

@@ -9,6 +9,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -880,25 +881,88 @@ static int check_gemm_args(const void* A, int a_bits, const int8_t* W, int M, in
   return EII_OK;
 }
 
-// Stream-ordered temporaries for the operator entry points (freed on the stream after use):
-// plain A [M, K] split into K-blocked limb planes, row-major W [N, K] in fragment order.
-struct Operands {
-  uint8_t* planes = nullptr;
-  int8_t* wf = nullptr;
-  hipStream_t s = nullptr;
-  ~Operands() {
-    if (planes) (void)hipFreeAsync(planes, s);
-    if (wf) (void)hipFreeAsync(wf, s);
+// Staging memory of the operator entry points (A split into K-blocked limb planes, W in fragment
+// order, column sums, requantization coefficients, V^T planes): one block per device, kept for
+// the life of the process and grown on demand, so calls at a size seen before allocate nothing.
+// Calls on one device take the block in turn: a call holds the host lock while it enqueues its
+// work, makes its stream wait for the event the previous call recorded (which may have been on
+// another stream) and records its own when it is done.  Growing frees the old block with
+// hipFree, which waits for the device to finish with it.
+constexpr int kMaxDevices = 64;
+struct StagingBlock {
+  uint8_t* p = nullptr;
+  size_t bytes = 0;
+  hipEvent_t done = nullptr;
+};
+static std::mutex g_staging_mu;
+static StagingBlock g_staging[kMaxDevices];
+
+class Staging {
+ public:
+  Staging() : lk_(g_staging_mu) {}
+  ~Staging() {
+    if (blk_) (void)hipEventRecord(blk_->done, s_);
   }
+  // The device's block, at least `bytes` long, for work enqueued on stream s.
+  int take(size_t bytes, hipStream_t s) {
+    int dev = 0;
+    HIPCHK(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices) return fail(EII_E_DEVICE, "device ordinal out of range");
+    StagingBlock& b = g_staging[dev];
+    if (!b.done) HIPCHK(hipEventCreateWithFlags(&b.done, hipEventDisableTiming));
+    else HIPCHK(hipStreamWaitEvent(s, b.done, 0));
+    if (b.bytes < bytes) {
+      if (b.p) HIPCHK(hipFree(b.p));
+      b.p = nullptr;
+      b.bytes = 0;
+      HIPCHK(hipMalloc((void**)&b.p, bytes));
+      b.bytes = bytes;
+    }
+    blk_ = &b;
+    s_ = s;
+    used_ = 0;
+    return EII_OK;
+  }
+  // Consecutive 256-byte aligned pieces of the block, in the order of the sizes given to take().
+  template <class T>
+  T* carve(size_t bytes) {
+    T* q = (T*)(blk_->p + used_);
+    used_ += align(bytes);
+    return q;
+  }
+  static size_t align(size_t bytes) { return (bytes + 255) & ~(size_t)255; }
+
+ private:
+  std::unique_lock<std::mutex> lk_;
+  StagingBlock* blk_ = nullptr;
+  hipStream_t s_ = nullptr;
+  size_t used_ = 0;
 };
 
-static int stage_operands(const void* A, int a_bits, const int8_t* W, int M, int N, int K, Operands& o, hipStream_t s) {
-  o.s = s;
-  HIPCHK(hipMallocAsync((void**)&o.planes, (size_t)M * K * (a_bits / 8), s));
-  HIPCHK(hipMallocAsync((void**)&o.wf, swizzled_bytes(N, K), s));
-  hipError_t e = split_limbs(A, a_bits / 8, M, K, o.planes, s);
-  if (e == hipSuccess) e = swizzle_weights(W, N, K, o.wf, s);
+static size_t operand_bytes(int a_bits, int M, int N, int K) {
+  return Staging::align((size_t)M * K * (a_bits / 8)) + Staging::align(swizzled_bytes(N, K));
+}
+
+// A [M, K] -> K-blocked limb planes, row-major W [N, K] -> fragment order, in the staging block.
+static int stage_operands(const void* A, int a_bits, const int8_t* W, int M, int N, int K, Staging& st,
+                          uint8_t*& planes, int8_t*& wf, hipStream_t s) {
+  planes = st.carve<uint8_t>((size_t)M * K * (a_bits / 8));
+  wf = st.carve<int8_t>(swizzled_bytes(N, K));
+  hipError_t e = split_limbs(A, a_bits / 8, M, K, planes, s);
+  if (e == hipSuccess) e = swizzle_weights(W, N, K, wf, s);
   if (e != hipSuccess) return fail(EII_E_DEVICE, std::string("operand staging: ") + hipGetErrorString(e));
+  return EII_OK;
+}
+
+static int gemm_i8_staged(const void* A, int a_bits, const int8_t* W, const int32_t* wsum, int M, int N, int K,
+                          int64_t* acc, Staging& st, hipStream_t s) {
+  uint8_t* planes;
+  int8_t* wf;
+  int rc;
+  if ((rc = stage_operands(A, a_bits, W, M, N, K, st, planes, wf, s))) return rc;
+  GemmArgs g{planes, wf, M, N, K, (size_t)M * K, wsum, nullptr, nullptr, acc, 64, nullptr};
+  hipError_t e = gemm(g, a_bits / 8, EPI_I64, s);
+  if (e != hipSuccess) return fail(EII_E_DEVICE, std::string("eii_gemm_i8: ") + hipGetErrorString(e));
   return EII_OK;
 }
 
@@ -909,27 +973,24 @@ extern "C" int eii_gemm_i8_ws(const void* A, int a_bits, const int8_t* W, const 
   if (!wsum || !acc) return fail(EII_E_ARG, "null output");
   if (N % 4) return fail(EII_E_ARG, "N must be a multiple of 4");
   hipStream_t s = (hipStream_t)stream;
-  Operands op;
-  if ((rc = stage_operands(A, a_bits, W, M, N, K, op, s))) return rc;
-  GemmArgs g{op.planes, op.wf, M, N, K, (size_t)M * K, wsum, nullptr, nullptr, acc, 64, nullptr};
-  hipError_t e = gemm(g, a_bits / 8, EPI_I64, s);
-  if (e != hipSuccess) return fail(EII_E_DEVICE, std::string("eii_gemm_i8: ") + hipGetErrorString(e));
-  return EII_OK;
+  Staging st;
+  if ((rc = st.take(operand_bytes(a_bits, M, N, K), s))) return rc;
+  return gemm_i8_staged(A, a_bits, W, wsum, M, N, K, acc, st, s);
 }
 
 extern "C" int eii_gemm_i8(const void* A, int a_bits, const int8_t* W, int M, int N, int K, int64_t* acc,
                            void* stream) {
   int rc;
   if ((rc = check_gemm_args(A, a_bits, W, M, N, K))) return rc;
+  if (!acc) return fail(EII_E_ARG, "null output");
+  if (N % 4) return fail(EII_E_ARG, "N must be a multiple of 4");
   hipStream_t s = (hipStream_t)stream;
-  int32_t* ws = nullptr;
-  HIPCHK(hipMallocAsync((void**)&ws, (size_t)N * 4, s));
-  rc = EII_OK;
+  Staging st;
+  if ((rc = st.take(operand_bytes(a_bits, M, N, K) + Staging::align((size_t)N * 4), s))) return rc;
+  int32_t* ws = st.carve<int32_t>((size_t)N * 4);
   hipError_t e = weight_colsum(W, N, K, ws, s);
-  if (e == hipSuccess) rc = eii_gemm_i8_ws(A, a_bits, W, ws, M, N, K, acc, stream);
-  else rc = fail(EII_E_DEVICE, hipGetErrorString(e));
-  (void)hipFreeAsync(ws, s);
-  return rc;
+  if (e != hipSuccess) return fail(EII_E_DEVICE, std::string("eii_gemm_i8: ") + hipGetErrorString(e));
+  return gemm_i8_staged(A, a_bits, W, ws, M, N, K, acc, st, s);
 }
 
 extern "C" int eii_linear(const void* A, int a_bits, const int8_t* W, const int32_t* wsum, const int32_t* mult,
@@ -940,18 +1001,19 @@ extern "C" int eii_linear(const void* A, int a_bits, const int8_t* W, const int3
   if (out_bits != 16 && out_bits != 32) return fail(EII_E_ARG, "out_bits must be 16 or 32");
   if (N % 4) return fail(EII_E_ARG, "N must be a multiple of 4");
   hipStream_t s = (hipStream_t)stream;
-  Operands op;
-  if ((rc = stage_operands(A, a_bits, W, M, N, K, op, s))) return rc;
-  GemmArgs g{op.planes, op.wf, M, N, K, (size_t)M * K, wsum, mult, shift, out, out_bits, nullptr};
-  double2* coef = nullptr;
+  Staging st;
+  if ((rc = st.take(operand_bytes(a_bits, M, N, K) + Staging::align((size_t)N * sizeof(double2)), s))) return rc;
+  uint8_t* planes;
+  int8_t* wf;
+  if ((rc = stage_operands(A, a_bits, W, M, N, K, st, planes, wf, s))) return rc;
+  GemmArgs g{planes, wf, M, N, K, (size_t)M * K, wsum, mult, shift, out, out_bits, nullptr};
   hipError_t e = hipSuccess;
   if (a_bits == 16) {
-    e = hipMallocAsync((void**)&coef, (size_t)N * sizeof(double2), s);
-    if (e == hipSuccess) e = gemm_coef(mult, shift, wsum, N, coef, s);
+    double2* coef = st.carve<double2>((size_t)N * sizeof(double2));
+    e = gemm_coef(mult, shift, wsum, N, coef, s);
     g.coef = coef;
   }
   if (e == hipSuccess) e = gemm(g, a_bits / 8, out_bits == 16 ? EPI_REQ16 : EPI_REQ32, s);
-  if (coef) (void)hipFreeAsync(coef, s);
   if (e != hipSuccess) return fail(EII_E_DEVICE, std::string("eii_linear: ") + hipGetErrorString(e));
   return EII_OK;
 }
@@ -990,12 +1052,12 @@ extern "C" int eii_attention(const int16_t* qkv, const int32_t* seq_off, int nse
     max_kt = std::max(max_kt, attn_key_tiles(off[i], T));
   }
   const int M = off[nseq];
-  uint8_t* vt = nullptr;
-  HIPCHK(hipMallocAsync((void**)&vt, vt_bytes(M), s));
+  Staging st;
+  if ((rc = st.take(vt_bytes(M), s))) return rc;
+  uint8_t* vt = st.carve<uint8_t>(vt_bytes(M));
   AttnArgs a{qkv, vt, seq_off, exp_tab, ctx, nullptr, M, nseq, max_T, max_kt, shift_s, 16 + f_v - f_c, bits_c};
   hipError_t e = build_vt(qkv, M, vt, s);
   if (e == hipSuccess) e = attention(a, s);
-  (void)hipFreeAsync(vt, s);
   if (e != hipSuccess) return fail(EII_E_DEVICE, std::string("eii_attention: ") + hipGetErrorString(e));
   return EII_OK;
 }

@@ -117,7 +117,12 @@ int eii_kv_append(eii_model* m, eii_kv* kv, const int64_t* ids_dev, int T_new, i
  * logits_dev int32 [rows, n] (numpy.argmax's tie rule). */
 int eii_argmax(const int32_t* logits_dev, int rows, int n, int64_t* out_dev, void* stream);
 
-/* ---- operator level (python/intref.py functions) ---- */
+/* ---- operator level (python/intref.py functions) ----
+ * eii_gemm_i8, eii_gemm_i8_ws, eii_linear and eii_attention stage their operands (limb planes,
+ * weights in fragment order, V^T planes) in one device block per GPU that the library keeps for
+ * the life of the process and grows with hipMalloc when a call needs more; calls at sizes seen
+ * before allocate nothing.  Calls on one GPU take the block in turn: each call's stream waits for
+ * the previous call's work, whichever stream that was on. */
 
 /* Row sums of int8 weights W_dev [N, K] into wsum_dev int32 [N]. */
 int eii_weight_colsum(const int8_t* W_dev, int N, int K, int32_t* wsum_dev, void* stream);

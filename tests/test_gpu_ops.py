@@ -50,6 +50,33 @@ def test_gemm_small(a_dtype, M, N, K):
     np.testing.assert_array_equal(got, exact_mm(A, W))
 
 
+def test_gemm_staging_two_streams():
+    # the operator entry points share one staging block per device: calls alternating between
+    # two streams, with sizes that grow (a new block) and shrink (the old one reused), are
+    # ordered by the block's event and each gives its own exact result
+    lib = L.load()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    cases = []
+    for i, (M, N, K, dt) in enumerate([(64, 80, 576, np.int16), (900, 576, 1536, np.int32), (33, 192, 576, np.int32),
+                                       (2000, 960, 576, np.int16), (5, 16, 64, np.int16), (700, 200, 128, np.int32)]):
+        rng = np.random.default_rng(100 + i)
+        info = np.iinfo(dt)
+        A = rng.integers(info.min, info.max, size=(M, K), endpoint=True, dtype=np.int64).astype(dt)
+        W = rng.integers(-127, 128, size=(N, K), dtype=np.int8)
+        At, Wt = dev(A), dev(W)
+        acc = torch.empty((M, N), dtype=torch.int64, device="cuda")
+        cases.append((A, W, At, Wt, acc))
+    torch.cuda.synchronize()
+    for i, (A, W, At, Wt, acc) in enumerate(cases):
+        s = streams[i % 2]
+        M, K = A.shape
+        L.check(lib.eii_gemm_i8(p(At), 16 if A.dtype == np.int16 else 32, p(Wt), M, W.shape[0], K, p(acc),
+                                C.c_void_p(s.cuda_stream)))
+    torch.cuda.synchronize()
+    for A, W, At, Wt, acc in cases:
+        np.testing.assert_array_equal(acc.cpu().numpy(), exact_mm(A, W))
+
+
 def test_gemm_layout_probe():
     # one-hot rows and columns: acc[m, n] picks single products, so a wrong lane/byte layout of
     # the MFMA operands shows up as a misplaced entry rather than a different sum

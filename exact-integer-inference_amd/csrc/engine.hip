@@ -1018,6 +1018,58 @@ extern "C" int eii_linear(const void* A, int a_bits, const int8_t* W, const int3
   return EII_OK;
 }
 
+extern "C" int eii_rope(int16_t* qkv, const int32_t* seq_off, int nseq, const int32_t* cosT, const int32_t* sinT,
+                        int rows, int f_q, int f_qr, int bits_qr, int f_k, int f_kr, int bits_kr, void* stream) {
+  if (!qkv || !seq_off || !cosT || !sinT || nseq <= 0 || rows <= 0) return fail(EII_E_ARG, "bad rope arguments");
+  if (bits_qr < 2 || bits_qr > 16 || bits_kr < 2 || bits_kr > 16)
+    return fail(EII_E_ARG, "rope outputs are int16: bits must be 2..16");
+  // |a1 c - a2 s| <= 2^46: a left shift of up to 16 stays inside int64
+  const int sh_q = 30 + f_q - f_qr, sh_k = 30 + f_k - f_kr;
+  if (sh_q < -16 || sh_q > 62 || sh_k < -16 || sh_k > 62) return fail(EII_E_BOUND, "rope shift out of range");
+  hipStream_t s = (hipStream_t)stream;
+  // positions restart at 0 in every sequence (python/intref.py:213): built on the host from the offsets
+  std::vector<int32_t> off(nseq + 1);
+  HIPCHK(hipMemcpyAsync(off.data(), seq_off, off.size() * 4, hipMemcpyDeviceToHost, s));
+  HIPCHK(hipStreamSynchronize(s));
+  std::vector<int32_t> pos;
+  for (int i = 0; i < nseq; ++i) {
+    const int T = off[i + 1] - off[i];
+    if (off[i] < 0 || T <= 0) return fail(EII_E_ARG, "seq_off must increase by at least 1 per sequence");
+    if (T > rows) return fail(EII_E_BOUND, "a sequence is longer than the RoPE rows given");
+    if (off[i] != (int)pos.size()) return fail(EII_E_ARG, "seq_off must start at 0 and be contiguous");
+    for (int t = 0; t < T; ++t) pos.push_back(t);
+  }
+  const int M = (int)pos.size();
+  Staging st;
+  int rc;
+  if ((rc = st.take((size_t)M * 4, s))) return rc;
+  int32_t* pos_dev = st.carve<int32_t>((size_t)M * 4);
+  HIPCHK(hipMemcpyAsync(pos_dev, pos.data(), (size_t)M * 4, hipMemcpyHostToDevice, s));
+  HIPCHK(rope(qkv, M, pos_dev, cosT, sinT, sh_q, bits_qr, sh_k, bits_kr, s));
+  HIPCHK(hipStreamSynchronize(s));   // the host positions die at return
+  return EII_OK;
+}
+
+extern "C" int eii_silu_gate(const int16_t* gate, const int16_t* up, int M, const int32_t* silu, int f_s, int f_u,
+                             int f_m, int bits_m, void* out, void* stream) {
+  if (!gate || !up || !silu || !out || M <= 0) return fail(EII_E_ARG, "bad silu gate arguments");
+  if (bits_m != 16 && bits_m != 32) return fail(EII_E_ARG, "bits_m must be 16 or 32");
+  // |silu u| < 2^46: a left shift of up to 16 stays inside int64
+  const int sh = f_s + f_u - f_m;
+  if (sh < -16 || sh > 62) return fail(EII_E_BOUND, "silu gate shift out of range");
+  hipStream_t s = (hipStream_t)stream;
+  Staging st;
+  int rc;
+  const size_t gu_bytes = (size_t)M * 2 * kDFF * 2;
+  if ((rc = st.take(gu_bytes, s))) return rc;
+  // the kernel reads rows of [gate 32 | up 32] blocks (the fused gate/up projection's layout)
+  int16_t* gu = st.carve<int16_t>(gu_bytes);
+  HIPCHK(hipMemcpy2DAsync(gu, 128, gate, 64, 64, (size_t)M * (kDFF / 32), hipMemcpyDeviceToDevice, s));
+  HIPCHK(hipMemcpy2DAsync((uint8_t*)gu + 64, 128, up, 64, 64, (size_t)M * (kDFF / 32), hipMemcpyDeviceToDevice, s));
+  HIPCHK(silu_gate(gu, M, silu, sh, bits_m, nullptr, out, s));
+  return EII_OK;
+}
+
 extern "C" int eii_rmsnorm(const int32_t* x, int M, const int32_t* gain, int f_gain, int f_out, int out_bits,
                            void* out, void* stream) {
   if (!x || !gain || !out || M <= 0) return fail(EII_E_ARG, "bad rmsnorm arguments");

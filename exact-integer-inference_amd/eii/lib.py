@@ -57,6 +57,8 @@ SIGNATURES = {
     "eii_linear": (i32, [vp, i32, vp, vp, vp, vp, i32, i32, i32, i32, vp, vp]),
     "eii_rmsnorm": (i32, [vp, i32, vp, i32, i32, i32, vp, vp]),
     "eii_attention": (i32, [vp, vp, i32, i32, vp, i32, i32, i32, i32, i32, vp, vp]),
+    "eii_rope": (i32, [vp, vp, i32, vp, vp, i32, i32, i32, i32, i32, i32, i32, vp]),
+    "eii_silu_gate": (i32, [vp, vp, i32, vp, i32, i32, i32, i32, vp, vp]),
 }
 
 _lib = None

@@ -156,6 +156,22 @@ int eii_attention(const int16_t* qkv_dev, const int32_t* seq_off_dev, int nseq, 
                   const int32_t* exp_tab_dev, int f_qr, int f_kr, int f_v, int f_c, int bits_c,
                   void* ctx_dev, void* stream);
 
+/* RoPE of one block (python/intref.py:212-225), in place on the q and k columns of qkv_dev
+ * int16 [M, 960] (q | k | v rows) for nseq sequences packed by seq_off_dev int32 [nseq + 1]
+ * (contiguous from row 0): row r of sequence i is position r - seq_off[i]. cos_dev, sin_dev
+ * int32 [rows, 32] hold rope_tables' Q30 values (python/intref.py:96-108). q heads:
+ * SAT(RS(., 30 + f_q - f_qr), bits_qr), k heads likewise with f_k, f_kr, bits_kr (bits <= 16). */
+int eii_rope(int16_t* qkv_dev, const int32_t* seq_off_dev, int nseq, const int32_t* cos_dev,
+             const int32_t* sin_dev, int rows, int f_q, int f_qr, int bits_qr, int f_k, int f_kr,
+             int bits_kr, void* stream);
+
+/* SiLU gate of the MLP (python/intref.py:272-276): out_dev [M, 1536] of bits_m (16 -> int16,
+ * 32 -> int32) = SAT(RS(silu_dev[g + 32768] * u, f_s + f_u - f_m), bits_m) for gate_dev and
+ * up_dev int16 [M, 1536] and silu_dev int32 [65536] (silu_table at the gate's format,
+ * python/intref.py:80-93); f_m is the gated format after the reference's min() for 32 bits. */
+int eii_silu_gate(const int16_t* gate_dev, const int16_t* up_dev, int M, const int32_t* silu_dev,
+                  int f_s, int f_u, int f_m, int bits_m, void* out_dev, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

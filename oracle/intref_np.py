@@ -57,6 +57,12 @@ def matmul_exact(A, W, bound_a, wmax=127):           # python/intref.py:58-63
     return np.rint(out).astype(I64)
 
 
+def silu_gate(silu, g, u, f_s, f_u, f_m, bits_m):   # python/intref.py:272-276
+    """SAT(RS(SILU[g + 32768] * u, f_s + f_u - f_m), bits_m), f_m already the reference's
+    min(f_m0, f_s + f_u) for 32-bit gated values."""
+    return sat(rs(silu[g + 32768] * u, f_s + f_u - f_m), bits_m)
+
+
 class OracleModel:
     """A model.bin image read into int64 numpy arrays (c/intref.c:70-91 read order)."""
 
@@ -236,7 +242,7 @@ class OracleModel:
         sg = Ly["silu"][g_ + 32768]
         bits_m, f_m0 = self.fmt("mlp_gated", l)
         f_m = min(f_m0, f_s + f_u) if bits_m == 32 else f_m0
-        gated = sat(rs(sg * u_, f_s + f_u - f_m), bits_m)
+        gated = silu_gate(Ly["silu"], g_, u_, f_s, f_u, f_m, bits_m)
         q_d, m_d, n_d = Ly["down"]
         acc = matmul_exact(gated, self.wf((l, "down"), q_d), 1 << (bits_m - 1))
         assert np.abs(acc).max() * int(m_d.max()) < 2 ** 63

@@ -45,6 +45,14 @@ def test_argument_errors_need_no_device():
     assert lib.eii_linear(a, 16, w, None, None, None, 1, 4, 64, 16, None, None) == L.EII_E_ARG
     assert lib.eii_rmsnorm(None, 1, None, 14, 11, 16, None, None) == L.EII_E_ARG
     assert lib.eii_attention(None, None, 1, 4, None, 10, 10, 11, 11, 16, None, None) == L.EII_E_ARG
+    assert lib.eii_rope(None, None, 1, None, None, 512, 10, 11, 16, 10, 11, 16, None) == L.EII_E_ARG
+    g = (C.c_int16 * 1536)()
+    t = (C.c_int32 * 65536)()
+    assert lib.eii_rope(g, t, 1, t, t, 512, 10, 11, 32, 10, 11, 16, None) == L.EII_E_ARG      # int16 out
+    assert lib.eii_rope(g, t, 1, t, t, 512, 10, 60, 16, 10, 11, 16, None) == L.EII_E_BOUND    # shift -20
+    assert lib.eii_silu_gate(None, None, 1, None, 12, 12, 13, 16, None, None) == L.EII_E_ARG
+    assert lib.eii_silu_gate(g, g, 1, t, 12, 12, 13, 8, g, None) == L.EII_E_ARG                # bits_m
+    assert lib.eii_silu_gate(g, g, 1, t, 12, 12, 60, 16, g, None) == L.EII_E_BOUND             # shift -36
     h = C.c_void_p()
     assert lib.eii_model_load(None, 0, C.byref(h)) == L.EII_E_ARG
     assert lib.eii_forward(None, None, 1, 1, None, None, None, None) == L.EII_E_ARG

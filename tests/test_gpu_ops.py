@@ -112,6 +112,70 @@ def test_rmsnorm(oracle):
         np.testing.assert_array_equal(out.cpu().numpy().astype(np.int64), want)
 
 
+@pytest.mark.parametrize("f_q,f_qr,bits_qr,f_k,f_kr,bits_kr", [
+    (10, 11, 16, 9, 9, 16),       # shifts 29 and 30
+    (10, 13, 16, 9, 12, 16),      # shifts 27: the rotated values saturate
+    (12, 11, 12, 9, 10, 10),      # narrower outputs
+    (2, 40, 16, 9, 45, 16),       # shifts -8 and -6: exact left shifts, saturating
+])
+def test_rope_operator(oracle, f_q, f_qr, bits_qr, f_k, f_kr, bits_kr):
+    # python/intref.py:212-225 on packed sequences: positions restart at 0 in each sequence
+    lib = L.load()
+    lens = [5, 160, 33, 1]
+    M = sum(lens)
+    rng = np.random.default_rng(f_qr * 100 + bits_qr)
+    qkv = rng.integers(-32768, 32768, size=(M, 960), dtype=np.int64)
+    qkv[0, :4] = [-32768, 32767, 0, -1]
+    qkv[1, 32:36] = [-32768, 32767, -32768, 32767]
+    off = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    qt, ot = dev(qkv.astype(np.int16)), dev(off)
+    ct, st = dev(oracle.rope_c.astype(np.int32)), dev(oracle.rope_s.astype(np.int32))
+    L.check(lib.eii_rope(p(qt), p(ot), len(lens), p(ct), p(st), oracle.rope_c.shape[0], f_q, f_qr, bits_qr, f_k, f_kr,
+                         bits_kr, None))
+    torch.cuda.synchronize()
+    got = qt.cpu().numpy().astype(np.int64)
+    pos = np.concatenate([np.arange(T) for T in lens])
+    np.testing.assert_array_equal(got[:, :576].reshape(M, 9, 64), oracle.rope(qkv[:, :576], 9, pos, f_q, f_qr, bits_qr))
+    np.testing.assert_array_equal(got[:, 576:768].reshape(M, 3, 64),
+                                  oracle.rope(qkv[:, 576:768], 3, pos, f_k, f_kr, bits_kr))
+    np.testing.assert_array_equal(got[:, 768:], qkv[:, 768:])   # v untouched
+
+
+def test_rope_operator_rows_bound(oracle):
+    lib = L.load()
+    qt = torch.zeros((600, 960), dtype=torch.int16, device="cuda")
+    ot = dev(np.array([0, 600], dtype=np.int32))
+    ct = dev(oracle.rope_c.astype(np.int32))
+    assert lib.eii_rope(p(qt), p(ot), 1, p(ct), p(ct), oracle.rope_c.shape[0], 10, 11, 16, 9, 9, 16, None) == \
+        L.EII_E_BOUND
+
+
+@pytest.mark.parametrize("f_g,f_s,bits_s,f_u,f_m,bits_m", [
+    (12, 13, 16, 12, 12, 16),     # shift 13
+    (10, 13, 16, 12, 25, 32),     # shift 0
+    (13, 14, 32, 11, 30, 32),     # 32-bit table, shift -5
+    (11, 13, 16, 12, 5, 16),      # shift 20
+    (9, 14, 16, 14, 14, 16),      # saturating products
+])
+def test_silu_gate_operator(f_g, f_s, bits_s, f_u, f_m, bits_m):
+    from eii.tables import silu_table
+    from oracle.intref_np import silu_gate
+    lib = L.load()
+    M = 37
+    rng = np.random.default_rng(f_m * 10 + bits_s)
+    g = rng.integers(-32768, 32768, size=(M, 1536), dtype=np.int64)
+    u = rng.integers(-32768, 32768, size=(M, 1536), dtype=np.int64)
+    g[0, :3] = [-32768, 32767, 0]
+    u[0, :3] = [-32768, -32768, 32767]
+    u[1, :] = 0
+    tab = np.asarray(silu_table(f_g, f_s, bits_s), dtype=np.int64)
+    out = torch.empty((M, 1536), dtype=torch.int16 if bits_m == 16 else torch.int32, device="cuda")
+    gt, ut, tt = dev(g.astype(np.int16)), dev(u.astype(np.int16)), dev(tab.astype(np.int32))
+    L.check(lib.eii_silu_gate(p(gt), p(ut), M, p(tt), f_s, f_u, f_m, bits_m, p(out), None))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(out.cpu().numpy().astype(np.int64), silu_gate(tab, g, u, f_s, f_u, f_m, bits_m))
+
+
 def _attention_case(oracle, lens, scale, seed, f_qr=10, f_kr=9, f_v=11, f_c=11, bits_c=16, floor=False):
     lib = L.load()
     rng = np.random.default_rng(seed)

@@ -127,7 +127,7 @@ int main(int argc, char** argv) {
       hipMalloc(&res, NL * TD * 4) != hipSuccess || hipMalloc(&lg, T * V * 4) != hipSuccess ||
       hipMemcpy(ids, idraw.data(), T * 8, hipMemcpyHostToDevice) != hipSuccess)
     return device_fail("device buffers");
-  if ((rc = eii_forward(m, ids, 1, (int)T, emb, res, lg, nullptr)) != EII_OK) {
+  if ((rc = eii_forward(m, ids, 1, (int)T, emb, res, lg, nullptr, nullptr)) != EII_OK) {
     fprintf(stderr, "forward: %s\n", eii_last_error());
     return rc == EII_E_DEVICE ? 3 : 2;
   }

@@ -663,8 +663,28 @@ int run_final(eii_model* m, const int32_t* x, int M, int32_t* logits, hipStream_
   return EII_OK;
 }
 
+// Row runs of the sequences whose states are dumped: (first row in the batch, first row in the
+// dump, rows); all sequences when mask is null.
+struct DumpRun {
+  size_t src, dst, rows;
+};
+
+std::vector<DumpRun> dump_runs(const std::vector<int32_t>& lens, const uint8_t* mask) {
+  std::vector<DumpRun> runs;
+  size_t src = 0, dst = 0;
+  for (size_t i = 0; i < lens.size(); ++i) {
+    if (!mask || mask[i]) {
+      if (!runs.empty() && runs.back().src + runs.back().rows == src) runs.back().rows += lens[i];
+      else runs.push_back({src, dst, (size_t)lens[i]});
+      dst += lens[i];
+    }
+    src += lens[i];
+  }
+  return runs;
+}
+
 int forward_impl(eii_model* m, const int64_t* ids, const std::vector<int32_t>& lens, int32_t* emb_out,
-                 int32_t* res_out, int32_t* logits, hipStream_t s) {
+                 int32_t* res_out, int32_t* logits, const uint8_t* dump_mask, hipStream_t s) {
   size_t M = 0;
   int max_T = 0;
   for (int32_t t : lens) {
@@ -683,14 +703,24 @@ int forward_impl(eii_model* m, const int64_t* ids, const std::vector<int32_t>& l
   int rc;
   if ((rc = ensure_ws(m, M)) || (rc = set_batch(m, lens, s))) return rc;
   const int Mi = (int)M;
+  const std::vector<DumpRun> runs = dump_runs(lens, dump_mask);
+  size_t dump_rows = 0;
+  for (const DumpRun& r : runs) dump_rows += r.rows;
+  auto dump = [&](int32_t* out) -> hipError_t {   // the selected rows of x, packed
+    for (const DumpRun& r : runs) {
+      hipError_t e = hipMemcpyAsync(out + r.dst * kD, m->x + r.src * kD, r.rows * kD * 4, hipMemcpyDeviceToDevice, s);
+      if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+  };
   {
     ProfScope ps(m, EII_K_EMBED, s);
     HIPCHK(embed(ids, Mi, m->emb_q, m->emb_m, m->emb_sh, m->x, m->flags, s));
   }
-  if (emb_out) HIPCHK(hipMemcpyAsync(emb_out, m->x, M * kD * 4, hipMemcpyDeviceToDevice, s));
+  if (emb_out) HIPCHK(dump(emb_out));
   for (int l = 0; l < kNL; ++l) {
     if ((rc = run_block(m, l, m->x, Mi, (int)lens.size(), max_T, nullptr, s))) return rc;
-    if (res_out) HIPCHK(hipMemcpyAsync(res_out + (size_t)l * M * kD, m->x, M * kD * 4, hipMemcpyDeviceToDevice, s));
+    if (res_out) HIPCHK(dump(res_out + (size_t)l * dump_rows * kD));
   }
   if (logits) return run_final(m, m->x, Mi, logits, s);
   return EII_OK;
@@ -699,17 +729,18 @@ int forward_impl(eii_model* m, const int64_t* ids, const std::vector<int32_t>& l
 }  // namespace
 
 extern "C" int eii_forward(eii_model* m, const int64_t* ids, int B, int T, int32_t* emb_out, int32_t* res_out,
-                           int32_t* logits, void* stream) {
+                           int32_t* logits, const uint8_t* dump_mask, void* stream) {
   if (!m || !ids || B <= 0 || T <= 0) return fail(EII_E_ARG, "bad forward arguments");
   std::vector<int32_t> lens(B, T);
-  return forward_impl(m, ids, lens, emb_out, res_out, logits, (hipStream_t)stream);
+  return forward_impl(m, ids, lens, emb_out, res_out, logits, dump_mask, (hipStream_t)stream);
 }
 
 extern "C" int eii_forward_packed(eii_model* m, const int64_t* ids, const int32_t* seq_lens, int nseq,
-                                  int32_t* emb_out, int32_t* res_out, int32_t* logits, void* stream) {
+                                  int32_t* emb_out, int32_t* res_out, int32_t* logits, const uint8_t* dump_mask,
+                                  void* stream) {
   if (!m || !ids || !seq_lens || nseq <= 0) return fail(EII_E_ARG, "bad forward arguments");
   std::vector<int32_t> lens(seq_lens, seq_lens + nseq);
-  return forward_impl(m, ids, lens, emb_out, res_out, logits, (hipStream_t)stream);
+  return forward_impl(m, ids, lens, emb_out, res_out, logits, dump_mask, (hipStream_t)stream);
 }
 
 // ------------------------------------------------------------------------------ decoding

@@ -73,29 +73,42 @@ class Engine:
             self.set_rope(max(T, 2 * self.rope_rows))
 
     # ------------------------------------------------------------------ forward
-    def forward(self, ids, embed=False, resid=False, logits=True, check=True):
+    def forward(self, ids, embed=False, resid=False, logits=True, check=True, dump=None):
         """ids int64 [B, T] (torch on the device, or numpy) -> dict of device tensors:
-        'embed' int32 [B, T, 576], 'resid' int32 [30, B, T, 576], 'logits' int32 [B, T, 49152]."""
+        'embed' int32 [S, T, 576], 'resid' int32 [30, S, T, 576], 'logits' int32 [B, T, 49152],
+        where the S dumped sequences are the indices in `dump` (in batch order; None = all B)."""
         ids = self._ids(ids)
         B, T = ids.shape
         self.ensure_rope(T)
-        out = self._alloc(B * T, embed, resid, logits)
+        mask = _dump_mask(B, dump)
+        S = B if mask is None else int(mask.sum())
+        out = self._alloc(S * T, embed, resid, False)
+        if logits:
+            out["logits"] = torch.empty((B * T, V), dtype=torch.int32, device=self.device)
         L.check(self.lib.eii_forward(self.h, _ptr(ids), B, T, _ptr(out.get("embed")), _ptr(out.get("resid")),
-                                     _ptr(out.get("logits")), _stream()))
+                                     _ptr(out.get("logits")), _mask_ptr(mask), _stream()))
         if check:
             self.check()
-        return self._shape(out, (B, T))
+        r = {k: (v.view(NL, S, T, -1) if k == "resid" else v.view(S, T, -1)) for k, v in out.items() if k != "logits"}
+        if logits:
+            r["logits"] = out["logits"].view(B, T, -1)
+        return r
 
-    def forward_packed(self, ids, seq_lens, embed=False, resid=False, logits=True, check=True):
-        """Ragged batch: ids int64 [sum(seq_lens)] packed sequence after sequence."""
+    def forward_packed(self, ids, seq_lens, embed=False, resid=False, logits=True, check=True, dump=None):
+        """Ragged batch: ids int64 [sum(seq_lens)] packed sequence after sequence; 'embed' and
+        'resid' hold the rows of the sequences in `dump` (None = all), packed."""
         ids = self._ids(ids).reshape(-1)
         lens = np.ascontiguousarray(seq_lens, dtype=np.int32)
         assert int(lens.sum()) == ids.numel()
         self.ensure_rope(int(lens.max()))
-        out = self._alloc(ids.numel(), embed, resid, logits)
+        mask = _dump_mask(len(lens), dump)
+        rows = ids.numel() if mask is None else int(lens[mask.astype(bool)].sum())
+        out = self._alloc(rows, embed, resid, False)
+        if logits:
+            out["logits"] = torch.empty((ids.numel(), V), dtype=torch.int32, device=self.device)
         L.check(self.lib.eii_forward_packed(self.h, _ptr(ids), lens.ctypes.data_as(L.i32p), len(lens),
                                             _ptr(out.get("embed")), _ptr(out.get("resid")),
-                                            _ptr(out.get("logits")), _stream()))
+                                            _ptr(out.get("logits")), _mask_ptr(mask), _stream()))
         if check:
             self.check()
         return out
@@ -190,6 +203,21 @@ class Engine:
         for k, v in out.items():
             r[k] = v.view(NL, B, T, -1) if k == "resid" else v.view(B, T, -1)
         return r
+
+
+def _dump_mask(n, dump):
+    """uint8 [n] with 1 at the sequence indices in dump, or None for every sequence."""
+    if dump is None:
+        return None
+    mask = np.zeros(n, dtype=np.uint8)
+    idx = np.asarray(dump, dtype=np.int64)
+    assert idx.size == 0 or (idx.min() >= 0 and idx.max() < n), "dump indices outside the batch"
+    mask[idx] = 1
+    return mask
+
+
+def _mask_ptr(mask):
+    return None if mask is None else mask.ctypes.data_as(C.c_void_p)
 
 
 class KVCache:

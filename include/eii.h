@@ -55,16 +55,20 @@ int eii_model_formats(const eii_model* m, int layer, int64_t* fm24, int64_t* f_y
 
 /* Batched forward (python/intref.py:288-301 for B independent sequences of T tokens).
  * ids_dev int64 [B*T].  Outputs, each optional (NULL = not written):
- *   embed_out_dev int32 [B*T, 576]; resid_out_dev int32 [30, B*T, 576] (after each block);
+ *   embed_out_dev int32 [S*T, 576]; resid_out_dev int32 [30, S*T, 576] (after each block);
  *   logits_dev int32 [B*T, 49152] (f = 16; exact when |logit| < 2^31, which
- *   python/export_vectors.py:58 asserts; eii_check reports a logit outside int32). */
+ *   python/export_vectors.py:58 asserts; eii_check reports a logit outside int32).
+ * dump_mask_host uint8 [B] (NULL = every sequence) selects the S sequences whose embedding and
+ * residual states are written, packed in batch order; logits cover every sequence. */
 int eii_forward(eii_model* m, const int64_t* ids_dev, int B, int T, int32_t* embed_out_dev,
-                int32_t* resid_out_dev, int32_t* logits_dev, void* stream);
+                int32_t* resid_out_dev, int32_t* logits_dev, const uint8_t* dump_mask_host,
+                void* stream);
 
-/* Ragged batch: seq_lens_host[nseq] tokens per sequence, ids packed sequence after sequence. */
+/* Ragged batch: seq_lens_host[nseq] tokens per sequence, ids packed sequence after sequence;
+ * dump_mask_host uint8 [nseq] as for eii_forward. */
 int eii_forward_packed(eii_model* m, const int64_t* ids_dev, const int32_t* seq_lens_host, int nseq,
                        int32_t* embed_out_dev, int32_t* resid_out_dev, int32_t* logits_dev,
-                       void* stream);
+                       const uint8_t* dump_mask_host, void* stream);
 
 /* Waits for `stream`, then reports data-dependent violations seen since the last check:
  * a token id outside [0, 49152) or a logit outside int32 (status 4). */

@@ -55,7 +55,7 @@ def test_argument_errors_need_no_device():
     assert lib.eii_silu_gate(g, g, 1, t, 12, 12, 60, 16, g, None) == L.EII_E_BOUND             # shift -36
     h = C.c_void_p()
     assert lib.eii_model_load(None, 0, C.byref(h)) == L.EII_E_ARG
-    assert lib.eii_forward(None, None, 1, 1, None, None, None, None) == L.EII_E_ARG
+    assert lib.eii_forward(None, None, 1, 1, None, None, None, None, None) == L.EII_E_ARG
     assert lib.eii_model_rope_rows(None) == 0
 
 

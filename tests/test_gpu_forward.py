@@ -52,6 +52,27 @@ def test_forward_cfg1(engine, oracle):
     assert first_diff(out["logits"].cpu().numpy(), lg) is None
 
 
+def test_forward_dump_selection(engine):
+    # the states of selected sequences, packed in batch order, equal their rows of a full dump;
+    # logits always cover the whole batch
+    rng = np.random.default_rng(12)
+    ids = rng.integers(0, 49152, size=(5, 40), dtype=np.int64)
+    full = engine.forward(ids, embed=True, resid=True, logits=True)
+    for sel in ([3], [0, 1, 4], [4, 2]):
+        part = engine.forward(ids, embed=True, resid=True, logits=True, dump=sel)
+        order = sorted(sel)
+        assert torch.equal(part["embed"], full["embed"][order])
+        assert torch.equal(part["resid"], full["resid"][:, order])
+        assert torch.equal(part["logits"], full["logits"])
+    lens = [7, 33, 1, 20]
+    flat = rng.integers(0, 49152, size=sum(lens), dtype=np.int64)
+    fullp = engine.forward_packed(flat, lens, embed=True, resid=True)
+    part = engine.forward_packed(flat, lens, embed=True, resid=True, dump=[1, 2])
+    assert torch.equal(part["embed"], fullp["embed"][7:41])
+    assert torch.equal(part["resid"], fullp["resid"][:, 7:41])
+    assert torch.equal(part["logits"], fullp["logits"])
+
+
 def test_forward_ragged_batch(engine, oracle):
     # sequences of different lengths packed in one forward equal their own B=1 runs
     rng = np.random.default_rng(11)

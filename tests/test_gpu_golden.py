@@ -31,15 +31,18 @@ def run_config(cfg, resid=True):
     eng = Engine(synth.ensure_model(kind), rope_rows=max(512, ids.shape[1]))
     out = None
     try:
-        out = eng.forward(ids, embed=True, resid=resid, logits=True)
+        # the embedding and residual states of the sampled sequences only (dump selection)
+        sampled = sorted(int(b) for b in GOLDEN[cfg]["sequences"])
+        out = eng.forward(ids, embed=True, resid=resid, logits=True, dump=sampled)
         torch.cuda.synchronize()
         bad = []
         for b, g in GOLDEN[cfg]["sequences"].items():
             b = int(b)
+            j = sampled.index(b)
             print(f"{cfg} sequence {b}", flush=True)
-            if sha(out["embed"][b]) != g["embed"]:
+            if sha(out["embed"][j]) != g["embed"]:
                 bad.append((b, "embed"))
-            if resid and sha(out["resid"][:, b]) != g["resid_out"]:
+            if resid and sha(out["resid"][:, j]) != g["resid_out"]:
                 bad.append((b, "resid_out"))
             if sha(out["logits"][b]) != g["logits"]:
                 bad.append((b, "logits"))
@@ -61,6 +64,5 @@ def test_cfg4_golden_sampled():
 
 
 def test_cfg5_golden_sampled():
-    # 131072 rows: the residual dump alone would be 9 GB, so the sampled sequences are checked on
-    # the embedding and the logits (whose digests cover every layer through the final state)
-    assert run_config("cfg5", resid=False) == []
+    # 131072 rows; the residual states of the 2 sampled sequences are 566 MB
+    assert run_config("cfg5") == []

@@ -1214,6 +1214,118 @@ __global__ __launch_bounds__(192) __attribute__((amdgpu_waves_per_eu(2))) void a
     }
 }
 
+// Decoding attention: one new query per sequence (the last of its kv_len cached rows) against
+// all of them, python/intref.py:227-254 with T = kv_len and only the last query row.  Workgroup =
+// one sequence and one kv group, wave w = query head 3 kvg + w.  Lane j scores keys j, j + 64, ...:
+// 64 int16 products summed exactly in int64, the SAT16 score kept in LDS; the wave's row max and
+// exp sum Z are reductions over the lanes; then, 64 keys at a time, each lane forms the probability
+// of one key (P = floor((e 65536 + floor(Z / 2)) / Z) from a float64 quotient and an exact
+// remainder correction) and the lanes, now one per head dimension, sum P v in int64 with each P
+// taken from its lane by v_readlane.  No key is masked: every cached key precedes the query.
+constexpr int kDecodeMaxKeys = 8192;   // scores of 3 waves x 8192 keys: 48 KB of LDS
+__host__ __device__ inline size_t attn_decode_lds(int L) {
+  return (size_t)(kDMax + 1 + 3) * 4 + (size_t)3 * ((L + 63) & ~63) * 2;
+}
+
+template <int OB>
+__global__ __launch_bounds__(192) void attn_decode_kernel(AttnArgs a) {
+  extern __shared__ __attribute__((aligned(16))) int32_t dsm[];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int seq = blockIdx.x, kvg = blockIdx.y, hh = 3 * kvg + w;
+  const int L = a.kv_len, Lp = (L + 63) & ~63;
+  int32_t* etab = dsm;
+  int16_t* sc = (int16_t*)(dsm + kDMax + 1 + 3) + (size_t)w * Lp;
+  for (int i = tid; i <= kDMax; i += 192) etab[i] = a.exp_tab[i];
+  const int16_t* base = a.qkv + (size_t)a.seq_off[seq] * kQKVN;   // key 0 of the sequence
+  const int4* q4 = (const int4*)(base + (size_t)(L - 1) * kQKVN + hh * 64);
+  int4 q[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) q[i] = q4[i];
+  __syncthreads();
+
+  // scores and the row max, two keys per lane and iteration so that their 16 loads are in flight
+  // together (a key past L re-reads key L - 1 and is not stored)
+  int32_t mx = INT32_MIN;
+  for (int j0 = lane; j0 < L; j0 += 128) {
+    int4 kk[2][8];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int4* k4 = (const int4*)(base + (size_t)min(j0 + 64 * u, L - 1) * kQKVN + kD + kvg * 64);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) kk[u][i] = k4[i];
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      int64_t acc = 0;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int32_t qw[4] = {q[i].x, q[i].y, q[i].z, q[i].w};
+        const int32_t kw[4] = {kk[u][i].x, kk[u][i].y, kk[u][i].z, kk[u][i].w};
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          acc += (int64_t)((int32_t)(int16_t)qw[r] * (int32_t)(int16_t)kw[r]);
+          acc += (int64_t)((qw[r] >> 16) * (kw[r] >> 16));
+        }
+      }
+      const int32_t s = (int32_t)sat(rs(acc, a.shift_s), 16);
+      if (j0 + 64 * u < L) {
+        sc[j0 + 64 * u] = (int16_t)s;
+        mx = max(mx, s);
+      }
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) mx = max(mx, __shfl_xor(mx, o));
+  // Z = sum of the table entries of d = max - s <= 1536 (entries beyond are 0); Z >= 2^30
+  int64_t Z = 0;
+  for (int j = lane; j < L; j += 64) {
+    const int d = mx - sc[j];
+    Z += d <= kDMax ? etab[d] : 0;
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) Z += __shfl_xor(Z, o);
+  const int64_t zh = Z >> 1;
+  const double zd = (double)Z;
+
+  // P v: lane = head dimension
+  const int16_t* vcol = base + kD + 192 + kvg * 64 + lane;
+  int64_t cacc = 0;
+  for (int c0 = 0; c0 < L; c0 += 64) {
+    int32_t P = 0;
+    if (c0 + lane < L) {
+      const int d = mx - sc[c0 + lane];
+      const int64_t num = (int64_t)(d <= kDMax ? etab[d] : 0) * 65536 + zh;   // < 2^47, exact in float64
+      int64_t qt = (int64_t)floor((double)num / zd);
+      const int64_t r = num - qt * Z;
+      qt += r < 0 ? -1 : (r >= Z ? 1 : 0);
+      P = (int32_t)qt;
+    }
+    // the 64 value rows of the chunk load together; rows past L re-read row L - 1 with P = 0
+    const int n = min(64, L - c0);
+    const int16_t* vr = vcol + (size_t)c0 * kQKVN;
+    int32_t vv[64];
+#pragma unroll
+    for (int jj = 0; jj < 64; ++jj) vv[jj] = vr[(size_t)min(jj, n - 1) * kQKVN];
+#pragma unroll
+    for (int jj = 0; jj < 64; ++jj) cacc += (int64_t)__builtin_amdgcn_readlane(P, jj) * vv[jj];
+  }
+
+  // SAT(RS(acc, sh_ctx), bits_c) in float64: |acc| < 2^45, exact wherever the result is not
+  // saturated (as in attn_kernel)
+  const double clo = -ldexp(1.0, a.bits_c - 1), chi = ldexp(1.0, a.bits_c - 1) - 1.0;
+  const int32_t cv = (int32_t)fmin(fmax(floor(fma((double)cacc, ldexp(1.0, -a.sh_ctx), 0.5)), clo), chi);
+  const int outM = a.out_M, qo = seq;   // one output row per sequence
+  const size_t pl = (size_t)outM * kD;
+  if (a.ctx_planes) {
+#pragma unroll
+    for (int l = 0; l < OB; ++l) a.ctx_planes[l * pl + plane_offset(qo, hh * 64 + lane, outM)] = (uint8_t)limb_byte(cv, l, OB);
+  }
+  if (a.ctx) {
+    if constexpr (OB == 2) ((int16_t*)a.ctx)[(size_t)qo * kD + hh * 64 + lane] = (int16_t)cv;
+    else ((int32_t*)a.ctx)[(size_t)qo * kD + hh * 64 + lane] = cv;
+  }
+}
+
 // V^T limb planes from qkv: thread = (d row, 4 consecutive token rows)
 __global__ __launch_bounds__(256) void vt_kernel(const int16_t* qkv, int M, uint8_t* vt, int stride) {
   const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x, ng = (size_t)stride / 4;
@@ -1315,6 +1427,13 @@ hipError_t attention(const AttnArgs& a, hipStream_t s) {
   // query tiles from the one holding q_first (0 for a plain forward) to the end
   const dim3 grid(a.B, kNKV, (a.max_T + 31) / 32 - (a.q_first >> 5)), block(192);
   // up to 8 key tiles (256 keys) the scores stay in registers; beyond, every pass recomputes them
+  if (a.kv_len && a.kv_len - a.q_first == 1 && a.kv_len <= kDecodeMaxKeys && a.out_M == a.B) {
+    // decoding step: one query per sequence
+    const size_t lds = attn_decode_lds(a.kv_len);
+    if (a.bits_c == 16) hipLaunchKernelGGL((attn_decode_kernel<2>), dim3(a.B, kNKV), dim3(192), lds, s, a);
+    else hipLaunchKernelGGL((attn_decode_kernel<4>), dim3(a.B, kNKV), dim3(192), lds, s, a);
+    return hipGetLastError();
+  }
   if (a.max_kt <= 5) {
     if (a.bits_c == 16) hipLaunchKernelGGL((attn_kernel<2, 5>), grid, block, 0, s, a);
     else hipLaunchKernelGGL((attn_kernel<4, 5>), grid, block, 0, s, a);

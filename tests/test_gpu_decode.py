@@ -74,6 +74,35 @@ def test_chunked_appends_equal_full_forward(eng, chunks):
         kv.close()
 
 
+def test_long_context_single_steps_equal_full_forward():
+    # single-token steps at cache lengths from 291 to 8194 on the stress model (q/k saturate, so
+    # many keys fall beyond the exp table): lengths up to 8192 take the one-query decoding
+    # kernel, longer ones the tiled attention; each step's logits equal the full forward's row
+    from eii.engine import Engine
+    T = 8194
+    e = Engine(synth.ensure_model("stress"), rope_rows=T)
+    try:
+        ids = torch.from_numpy(np.random.default_rng(8).integers(0, 49152, size=(2, T), dtype=np.int64)).to(e.device)
+        full = e.forward(ids)["logits"]
+        kv = e.kv_cache(2, T)
+        try:
+            t = 0
+            for start, steps in ((290, 3), (1029, 2), (8190, 4)):
+                print(f"append {t}..{start - 1}, then {steps} single steps", flush=True)
+                kv.append(ids[:, t:start], logits=False)
+                t = start
+                for _ in range(steps):
+                    lg = kv.append(ids[:, t:t + 1])
+                    assert torch.equal(lg[:, 0], full[:, t]), t
+                    t += 1
+        finally:
+            kv.close()
+    finally:
+        del full
+        e.close()
+        torch.cuda.empty_cache()
+
+
 def test_greedy_trajectory_cached_equals_recomputed(eng):
     prompt = torch.from_numpy(synth.token_ids("cfg4")[[0, 111], :128]).to(eng.device)
     toks, lg = eng.generate(prompt, 32)

@@ -3,9 +3,13 @@ libeii_hostcheck.so in place.
 
     python build.py                              # everything, next to this file
     python build.py --out DIR --opt="-O1 ..."    # libeii.so + eii_check into DIR, the HIP
-                                                 # sources compiled with these optimization flags
-                                                 # instead of -O3 (the build variants of
-                                                 # python -m eii.conformance)
+                                                 # sources and the checker compiled with these
+                                                 # optimization flags instead of -O3 / -O2 (the
+                                                 # build variants of python -m eii.conformance)
+
+hipcc applies a plain -O level to the host and the device code alike; "-Xarch_host -O0" after it
+lowers the host code only (the engine, the C ABI and the checker) and leaves the device code at
+the level before it.
 """
 import argparse
 import os
@@ -43,10 +47,10 @@ def build_lib(out=HERE, opt=OPT):
     os.replace(lib + ".tmp", lib)
 
 
-def build_checker(out=HERE):
+def build_checker(out=HERE, opt=("-O2",)):
     checker = os.path.join(out, "eii_check")
-    run([HIPCC, "-O2", "-std=c++17", "-Wall", "-I" + INCLUDE, os.path.join(CSRC, "eii_check.cpp"),
-         "-L" + out, "-leii", "-Wl,-rpath,$ORIGIN", "-o", checker + ".tmp"])
+    run([HIPCC] + list(opt) + ["-std=c++17", "-Wall", "-I" + INCLUDE, os.path.join(CSRC, "eii_check.cpp"),
+                               "-L" + out, "-leii", "-Wl,-rpath,$ORIGIN", "-o", checker + ".tmp"])
     os.replace(checker + ".tmp", checker)
 
 
@@ -72,7 +76,7 @@ def main(argv=None):
         out = os.path.abspath(a.out or HERE)
         os.makedirs(out, exist_ok=True)
         build_lib(out, shlex.split(a.opt))
-        build_checker(out)
+        build_checker(out, shlex.split(a.opt))
     return 0
 
 

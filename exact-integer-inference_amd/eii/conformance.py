@@ -16,10 +16,13 @@ The steps of tools/record_conformance.sh:17-84, on an MI355X:
   exp_resid_out.i32 (record_conformance.sh:44-63) must be reported with exit status 1 and a
   DIFFERS or MISMATCH line;
 * build variants: libeii.so and eii_check rebuilt from the sources with other optimization
-  flags (default "-O1" and "-O2 -ffp-contract=off"), each exact on every set
-  (record_conformance.sh:65-78).  An unoptimized -O0 build is not possible here: the LDS DMA
-  and scalar-register operands of the GEMM need values the compiler proves uniform, which it
-  does only when optimizing.
+  flags, each exact on every set (record_conformance.sh:65-78).  Defaults:
+  "-O3 -Xarch_host -O0": the host code (engine, C ABI, checker) unoptimized and the device code
+  optimized, which is what the reference's "nvcc -O0" variant builds (nvcc's -O sets the host
+  compiler's level; the device assembler keeps its default optimization); "-O1" and
+  "-O2 -ffp-contract=off" for host and device code alike.  Device code cannot be built at -O0:
+  the LDS DMA and scalar-register operands of the GEMM need values the compiler proves
+  uniform, which it does only when optimizing.
 
 Everything is printed and appended to DIR/run-YYYYmmdd-HHMMSS.txt (default DIR:
 ./conformance_runs); the last lines are RECORD OK or RECORD HAS FAILURES and the record's path.
@@ -41,7 +44,7 @@ from .export_vectors import hash_root
 
 PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 CHECKER = os.path.join(PKG, "eii_check")
-DEFAULT_VARIANTS = ("-O1", "-O2 -ffp-contract=off")
+DEFAULT_VARIANTS = ("-O3 -Xarch_host -O0", "-O1", "-O2 -ffp-contract=off")
 DEFAULT_SETS = ("t24", "t128", "t160")
 EXACT = "ALL STATES EXACT"
 

@@ -1216,99 +1216,122 @@ __global__ __launch_bounds__(192) __attribute__((amdgpu_waves_per_eu(2))) void a
 
 // Decoding attention: one new query per sequence (the last of its kv_len cached rows) against
 // all of them, python/intref.py:227-254 with T = kv_len and only the last query row.  Workgroup =
-// one sequence and one kv group, wave w = query head 3 kvg + w.  Lane j scores keys j, j + 64, ...:
-// 64 int16 products summed exactly in int64, the SAT16 score kept in LDS; the wave's row max and
-// exp sum Z are reductions over the lanes; then, 64 keys at a time, each lane forms the probability
-// of one key (P = floor((e 65536 + floor(Z / 2)) / Z) from a float64 quotient and an exact
-// remainder correction) and the lanes, now one per head dimension, sum P v in int64 with each P
-// taken from its lane by v_readlane.  No key is masked: every cached key precedes the query.
-constexpr int kDecodeMaxKeys = 8192;   // scores of 3 waves x 8192 keys: 48 KB of LDS
-__host__ __device__ inline size_t attn_decode_lds(int L) {
-  return (size_t)(kDMax + 1 + 3) * 4 + (size_t)3 * ((L + 63) & ~63) * 2;
+// one sequence and one kv group: NW waves per query head 3 kvg + hq (NW = 4 for few sequences,
+// where the latency of one workgroup is the step's; 1 when the sequences fill the GPU); the keys
+// go in 64-key chunks, chunk c to wave c % NW of each head.  Lane j of a wave scores key 64 c + j (64 int16
+// products summed exactly in int64; the SAT16 score kept in LDS) and, once the row max and the exp
+// sum Z are known (wave reductions, then the head's 4 waves through LDS), forms its key's
+// probability P = floor((e 65536 + floor(Z / 2)) / Z) from a float64 quotient and an exact
+// remainder correction; the lanes then, one per head dimension, sum P v over the chunk in int64
+// with each P taken from its lane by v_readlane, and the head's 4 partial sums meet in LDS.  A
+// wave's first value chunk is loaded before the reductions, so its latency hides behind them.
+// No key is masked: every cached key precedes the query.
+constexpr int kDecodeMaxKeys = 8192;   // scores of 3 heads x 8192 keys: 48 KB of LDS
+__host__ __device__ inline size_t attn_decode_lds(int L, int NW) {
+  return (size_t)(kDMax + 1 + 3) * 4 + (size_t)3 * NW * (4 + 8 + 64 * 8) + (size_t)3 * ((L + 63) & ~63) * 2;
 }
 
-template <int OB>
-__global__ __launch_bounds__(192) void attn_decode_kernel(AttnArgs a) {
+template <int OB, int NW>
+__global__ __launch_bounds__(64 * 3 * NW) void attn_decode_kernel(AttnArgs a) {
   extern __shared__ __attribute__((aligned(16))) int32_t dsm[];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int seq = blockIdx.x, kvg = blockIdx.y, hh = 3 * kvg + w;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, hq = w / NW, kw = w % NW;
+  const int seq = blockIdx.x, kvg = blockIdx.y, hh = 3 * kvg + hq;
   const int L = a.kv_len, Lp = (L + 63) & ~63;
-  int32_t* etab = dsm;
-  int16_t* sc = (int16_t*)(dsm + kDMax + 1 + 3) + (size_t)w * Lp;
-  for (int i = tid; i <= kDMax; i += 192) etab[i] = a.exp_tab[i];
+  int32_t* etab = dsm;                                          // [1537] (+3 pad)
+  int32_t* smax = dsm + kDMax + 1 + 3;                          // [12]
+  int64_t* sz = (int64_t*)(smax + 3 * NW);                      // [12]
+  int64_t* spart = sz + 3 * NW;                                 // [12][64]
+  int16_t* sc = (int16_t*)(spart + 3 * NW * 64) + (size_t)hq * Lp;
+  for (int i = tid; i <= kDMax; i += 64 * 3 * NW) etab[i] = a.exp_tab[i];
   const int16_t* base = a.qkv + (size_t)a.seq_off[seq] * kQKVN;   // key 0 of the sequence
   const int4* q4 = (const int4*)(base + (size_t)(L - 1) * kQKVN + hh * 64);
   int4 q[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) q[i] = q4[i];
-  __syncthreads();
 
-  // scores and the row max, two keys per lane and iteration so that their 16 loads are in flight
-  // together (a key past L re-reads key L - 1 and is not stored)
+  // scores of this wave's chunks and their max (a key past L re-reads key L - 1, not stored)
   int32_t mx = INT32_MIN;
-  for (int j0 = lane; j0 < L; j0 += 128) {
-    int4 kk[2][8];
+  for (int c = kw; 64 * c < L; c += NW) {
+    const int j = 64 * c + lane;
+    const int4* k4 = (const int4*)(base + (size_t)min(j, L - 1) * kQKVN + kD + kvg * 64);
+    int4 kk[8];
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int4* k4 = (const int4*)(base + (size_t)min(j0 + 64 * u, L - 1) * kQKVN + kD + kvg * 64);
+    for (int i = 0; i < 8; ++i) kk[i] = k4[i];
+    int64_t acc = 0;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) kk[u][i] = k4[i];
-    }
+    for (int i = 0; i < 8; ++i) {
+      const int32_t qw[4] = {q[i].x, q[i].y, q[i].z, q[i].w}, kw4[4] = {kk[i].x, kk[i].y, kk[i].z, kk[i].w};
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      int64_t acc = 0;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int32_t qw[4] = {q[i].x, q[i].y, q[i].z, q[i].w};
-        const int32_t kw[4] = {kk[u][i].x, kk[u][i].y, kk[u][i].z, kk[u][i].w};
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          acc += (int64_t)((int32_t)(int16_t)qw[r] * (int32_t)(int16_t)kw[r]);
-          acc += (int64_t)((qw[r] >> 16) * (kw[r] >> 16));
-        }
-      }
-      const int32_t s = (int32_t)sat(rs(acc, a.shift_s), 16);
-      if (j0 + 64 * u < L) {
-        sc[j0 + 64 * u] = (int16_t)s;
-        mx = max(mx, s);
+      for (int r = 0; r < 4; ++r) {
+        acc += (int64_t)((int32_t)(int16_t)qw[r] * (int32_t)(int16_t)kw4[r]);
+        acc += (int64_t)((qw[r] >> 16) * (kw4[r] >> 16));
       }
     }
+    const int32_t sv = (int32_t)sat(rs(acc, a.shift_s), 16);
+    if (j < L) {
+      sc[j] = (int16_t)sv;
+      mx = max(mx, sv);
+    }
+  }
+  // the value rows of this wave's first chunk, loaded now (rows past L re-read row L - 1)
+  const int16_t* vcol = base + kD + 192 + kvg * 64 + lane;
+  int32_t vv[64];
+  if (64 * kw < L) {
+    const int n = min(64, L - 64 * kw);
+#pragma unroll
+    for (int jj = 0; jj < 64; ++jj) vv[jj] = vcol[(size_t)(64 * kw + min(jj, n - 1)) * kQKVN];
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) mx = max(mx, __shfl_xor(mx, o));
+  if (lane == 0) smax[w] = mx;
+  __syncthreads();
+  mx = smax[hq * NW];
+#pragma unroll
+  for (int k = 1; k < NW; ++k) mx = max(mx, smax[hq * NW + k]);
   // Z = sum of the table entries of d = max - s <= 1536 (entries beyond are 0); Z >= 2^30
   int64_t Z = 0;
-  for (int j = lane; j < L; j += 64) {
-    const int d = mx - sc[j];
-    Z += d <= kDMax ? etab[d] : 0;
+  for (int c = kw; 64 * c < L; c += NW) {
+    const int j = 64 * c + lane;
+    if (j < L) {
+      const int d = mx - sc[j];
+      Z += d <= kDMax ? etab[d] : 0;
+    }
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) Z += __shfl_xor(Z, o);
+  if (lane == 0) sz[w] = Z;
+  __syncthreads();
+  Z = 0;
+#pragma unroll
+  for (int k = 0; k < NW; ++k) Z += sz[hq * NW + k];
   const int64_t zh = Z >> 1;
   const double zd = (double)Z;
 
-  // P v: lane = head dimension
-  const int16_t* vcol = base + kD + 192 + kvg * 64 + lane;
+  // P v over this wave's chunks: lane = head dimension
   int64_t cacc = 0;
-  for (int c0 = 0; c0 < L; c0 += 64) {
+  for (int c = kw; 64 * c < L; c += NW) {
+    const int j = 64 * c + lane, n = min(64, L - 64 * c);
+    if (c != kw) {
+#pragma unroll
+      for (int jj = 0; jj < 64; ++jj) vv[jj] = vcol[(size_t)(64 * c + min(jj, n - 1)) * kQKVN];
+    }
     int32_t P = 0;
-    if (c0 + lane < L) {
-      const int d = mx - sc[c0 + lane];
+    if (j < L) {
+      const int d = mx - sc[j];
       const int64_t num = (int64_t)(d <= kDMax ? etab[d] : 0) * 65536 + zh;   // < 2^47, exact in float64
       int64_t qt = (int64_t)floor((double)num / zd);
       const int64_t r = num - qt * Z;
       qt += r < 0 ? -1 : (r >= Z ? 1 : 0);
       P = (int32_t)qt;
     }
-    // the 64 value rows of the chunk load together; rows past L re-read row L - 1 with P = 0
-    const int n = min(64, L - c0);
-    const int16_t* vr = vcol + (size_t)c0 * kQKVN;
-    int32_t vv[64];
-#pragma unroll
-    for (int jj = 0; jj < 64; ++jj) vv[jj] = vr[(size_t)min(jj, n - 1) * kQKVN];
 #pragma unroll
     for (int jj = 0; jj < 64; ++jj) cacc += (int64_t)__builtin_amdgcn_readlane(P, jj) * vv[jj];
   }
+  spart[w * 64 + lane] = cacc;
+  __syncthreads();
+  if (kw != 0) return;
+#pragma unroll
+  for (int k = 1; k < NW; ++k) cacc += spart[(w + k) * 64 + lane];
 
   // SAT(RS(acc, sh_ctx), bits_c) in float64: |acc| < 2^45, exact wherever the result is not
   // saturated (as in attn_kernel)
@@ -1429,9 +1452,17 @@ hipError_t attention(const AttnArgs& a, hipStream_t s) {
   // up to 8 key tiles (256 keys) the scores stay in registers; beyond, every pass recomputes them
   if (a.kv_len && a.kv_len - a.q_first == 1 && a.kv_len <= kDecodeMaxKeys && a.out_M == a.B) {
     // decoding step: one query per sequence
-    const size_t lds = attn_decode_lds(a.kv_len);
-    if (a.bits_c == 16) hipLaunchKernelGGL((attn_decode_kernel<2>), dim3(a.B, kNKV), dim3(192), lds, s, a);
-    else hipLaunchKernelGGL((attn_decode_kernel<4>), dim3(a.B, kNKV), dim3(192), lds, s, a);
+    // 4 waves per head while the workgroups (3 per sequence) leave most CUs idle
+    const dim3 grid(a.B, kNKV);
+    if (3 * a.B < 256) {
+      const size_t lds = attn_decode_lds(a.kv_len, 4);
+      if (a.bits_c == 16) hipLaunchKernelGGL((attn_decode_kernel<2, 4>), grid, dim3(768), lds, s, a);
+      else hipLaunchKernelGGL((attn_decode_kernel<4, 4>), grid, dim3(768), lds, s, a);
+    } else {
+      const size_t lds = attn_decode_lds(a.kv_len, 1);
+      if (a.bits_c == 16) hipLaunchKernelGGL((attn_decode_kernel<2, 1>), grid, dim3(192), lds, s, a);
+      else hipLaunchKernelGGL((attn_decode_kernel<4, 1>), grid, dim3(192), lds, s, a);
+    }
     return hipGetLastError();
   }
   if (a.max_kt <= 5) {

@@ -74,6 +74,20 @@ def test_chunked_appends_equal_full_forward(eng, chunks):
         kv.close()
 
 
+def test_many_sequences_single_steps_equal_full_forward(eng):
+    # 96 sequences: the decoding attention runs one wave per head (few sequences take four)
+    ids = torch.from_numpy(np.random.default_rng(96).integers(0, 49152, size=(96, 70), dtype=np.int64)).to(eng.device)
+    full = eng.forward(ids)["logits"]
+    kv = eng.kv_cache(96, 70)
+    try:
+        kv.append(ids[:, :64], logits=False)
+        for t in range(64, 70):
+            lg = kv.append(ids[:, t:t + 1])
+            assert torch.equal(lg[:, 0], full[:, t]), t
+    finally:
+        kv.close()
+
+
 def test_long_context_single_steps_equal_full_forward():
     # single-token steps at cache lengths from 291 to 8194 on the stress model (q/k saturate, so
     # many keys fall beyond the exp table): lengths up to 8192 take the one-query decoding

@@ -116,7 +116,9 @@ def write(path, emb_q, emb_m, emb_n, final_gain, f_y, exp_tab, rope_cos, rope_si
     def w(f, a, dt):
         f.write(np.ascontiguousarray(a, dtype=dt).tobytes())
 
-    tmp = path + ".tmp"
+    # A per-process temporary name: several processes may generate the same cached model at once
+    # (parallel test workers); each renames its own complete file into place.
+    tmp = "%s.%d.tmp" % (path, os.getpid())
     with open(tmp, "wb") as f:
         w(f, emb_q, np.int8); w(f, emb_m, "<i8"); w(f, emb_n, "<i8")
         w(f, final_gain[0], "<i8"); w(f, [final_gain[1]], "<i8"); w(f, [f_y], "<i8")

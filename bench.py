@@ -6,9 +6,11 @@ A step is one full forward (embedding, 30 blocks, final norm, tied head with int
 over the configuration's whole batch of synthetic token ids, with the ids already in HBM.
 Prints one JSON line.  The dominant kernel class is timed live with HIP events recorded on
 its launch stream over the timed steps, and its roofline fraction is reported against the
-int8 MFMA peak.  The CPU baseline runs the reference's own C program (c/intref.c, compiled
-into oracle/_ref/intref by oracle/Makefile) on one sequence of the same workload, checking
-the GPU's states at the same time; without that binary it times the numpy oracle instead.
+int8 MFMA peak on the algorithmic count (2 M N K per projection).  The CPU baseline runs the
+reference's own C program (c/intref.c, compiled into oracle/_ref/intref by oracle/Makefile) on
+one thread over a sample of the same workload's sequences, checking the GPU's states at the same
+time; beside it, on the same sample: the integer C restatement (oracle/intref_c.c) on all the
+host's threads and the numpy oracle with one and with all BLAS threads.
 """
 import argparse
 import hashlib
@@ -31,6 +33,7 @@ REF_BIN = os.path.join(ROOT, "oracle", "_ref", "intref")
 GOLDEN = os.path.join(ROOT, "tests", "golden", "golden.json")
 PROFILES = os.path.join(ROOT, "profiles")
 COPY_BYTES = 1 << 30            # --copy-calibration: one plain device copy of 1 GiB
+CPU_SEQS = 4                    # sequences in the CPU baseline's sample (about 25 s for the reference C)
 
 
 def sha(a):
@@ -58,26 +61,114 @@ def gemm_ops(engine, M):
     return ops
 
 
-def cpu_baseline_reference(model_path, ids, out):
-    """Run the reference's C checker on sequence 0 with the GPU's states as the expected ones."""
+def cpu_baseline_reference(model_path, ids, out, sample):
+    """Run the reference's C checker on the sampled sequences with the GPU's states as the expected
+    ones; sample = [(batch index, dump index)]."""
     T = ids.shape[1]
-    with tempfile.TemporaryDirectory() as d:
-        ids[0].astype(np.int64).tofile(os.path.join(d, "ids.i64"))
-        out["embed"][0].cpu().numpy().astype(np.int32).tofile(os.path.join(d, "exp_embed.i32"))
-        out["resid"][:, 0].cpu().numpy().astype(np.int32).tofile(os.path.join(d, "exp_resid_out.i32"))
-        out["logits"][0].cpu().numpy().astype(np.int32).tofile(os.path.join(d, "exp_logits.i32"))
-        os.symlink(os.path.abspath(model_path), os.path.join(d, "model.bin"))
-        t0 = time.perf_counter()
-        r = subprocess.run([REF_BIN, d, d], capture_output=True, text=True, timeout=600)
-        wall = time.perf_counter() - t0
-    last = r.stdout.strip().splitlines()[-1] if r.stdout.strip() else ""
-    cpu_s = wall
-    if "(" in last and " s)" in last:
-        cpu_s = float(last.split(",")[-1].split()[0])
-    return {"value": T / cpu_s, "unit": "tokens/s", "cores": 1, "kind": "reference",
-            "sample": f"1 sequence x {T} tokens of the benchmark batch (sequence 0), full 30-layer forward + "
-                      f"head, reference c/intref.c -O2 on 1 host thread, its clock() CPU time",
-            "seconds": cpu_s, "wall_seconds": wall, "verdict": last, "states_checked_by_reference": r.returncode == 0}
+    cpu_s = wall = 0.0
+    verdicts, ok = [], True
+    for b, j in sample:
+        with tempfile.TemporaryDirectory() as d:
+            _write_vectors(d, model_path, ids, out, b, j)
+            t0 = time.perf_counter()
+            r = subprocess.run([REF_BIN, d, d], capture_output=True, text=True, timeout=600)
+            w = time.perf_counter() - t0
+        last = r.stdout.strip().splitlines()[-1] if r.stdout.strip() else ""
+        s = w
+        if "(" in last and " s)" in last:
+            s = float(last.split(",")[-1].split()[0])
+        cpu_s += s
+        wall += w
+        verdicts.append(last)
+        ok = ok and r.returncode == 0
+    n = len(sample) * T
+    return {"value": n / cpu_s, "unit": "tokens/s", "cores": 1, "kind": "reference",
+            "sample": f"{len(sample)} sequences x {T} tokens of the benchmark batch (sequences "
+                      f"{[b for b, _ in sample]}), full 30-layer forward + head, reference c/intref.c -O2 on 1 host "
+                      f"thread, its clock() CPU time", "seconds": cpu_s, "wall_seconds": wall, "verdicts": verdicts,
+            "states_checked_by_reference": ok}
+
+
+ORACLE_C = os.path.join(ROOT, "oracle", "_build", "intref_c")
+
+
+def host_cpu():
+    """The host's CPU model, logical CPU count and the thread share the benchmark uses for its
+    all-core legs (OMP_NUM_THREADS when the environment sets it, else every logical CPU)."""
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    n = os.cpu_count() or 1
+    share = int(os.environ.get("OMP_NUM_THREADS") or n)
+    return {"model": model, "logical_cpus": n, "threads_used_all_core": share}
+
+
+def _thread_env(n):
+    env = dict(os.environ)
+    for k in ("OMP_NUM_THREADS", "OPENBLAS_NUM_THREADS", "MKL_NUM_THREADS", "BLIS_NUM_THREADS"):
+        env[k] = str(n)
+    return env
+
+
+def cpu_leg_c_restatement(model_path, ids, out, sample, threads):
+    """oracle/intref_c (integer-only C restatement, OpenMP) on the sampled sequences, each checking
+    the GPU's states."""
+    T = ids.shape[1]
+    wall, ok, last = 0.0, True, ""
+    for b, j in sample:
+        with tempfile.TemporaryDirectory() as d:
+            _write_vectors(d, model_path, ids, out, b, j)
+            t0 = time.perf_counter()
+            r = subprocess.run([ORACLE_C, d, d], capture_output=True, text=True, timeout=600,
+                               env=_thread_env(threads))
+            wall += time.perf_counter() - t0
+        last = r.stdout.strip().splitlines()[-1] if r.stdout.strip() else ""
+        ok = ok and r.returncode == 0
+    return {"value": len(sample) * T / wall, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "what": f"oracle/intref_c.c (integer-only C restatement, -O2 -fopenmp) on {threads} threads, wall time "
+                    f"including each run's model.bin read", "seconds": wall, "last_verdict": last,
+            "states_checked": ok}
+
+
+def cpu_leg_numpy(ids, sample, threads, model_path):
+    """The numpy oracle (float64 BLAS exact products, the algorithm class of python/intref.py) on the
+    sampled sequences in a child process whose BLAS runs `threads` threads; model parsing not timed."""
+    seqs = ";".join(",".join(str(int(i)) for i in ids[b]) for b, _ in sample)
+    r = subprocess.run([sys.executable, os.path.abspath(__file__), "--cpu-numpy-leg", model_path, seqs],
+                       capture_output=True, text=True, timeout=900, env=_thread_env(threads))
+    rec = json.loads(r.stdout.strip().splitlines()[-1])
+    n = len(sample) * ids.shape[1]
+    return {"value": n / rec["seconds"], "unit": "tokens/s", "cores": threads, "kind": "port",
+            "what": f"numpy oracle (oracle/intref_np.py, float64 BLAS exact products, per-head and per-row loops) "
+                    f"with {threads} BLAS thread(s)", "seconds": rec["seconds"],
+            "load_seconds": rec["load_seconds"]}
+
+
+def numpy_leg_child(model_path, ids_csv):
+    sys.path.insert(0, ROOT)
+    t0 = time.perf_counter()
+    from oracle.intref_np import OracleModel
+    M = OracleModel(model_path)
+    seqs = [np.array([int(v) for v in q.split(",")], dtype=np.int64)[None, :] for q in ids_csv.split(";")]
+    t1 = time.perf_counter()
+    for ids in seqs:
+        M.forward(ids)
+    t2 = time.perf_counter()
+    print(json.dumps({"seconds": t2 - t1, "load_seconds": t1 - t0}))
+
+
+def _write_vectors(d, model_path, ids, out, b=0, j=0):
+    """Vector directory of batch sequence b (dumped as index j of the forward's dump list)."""
+    ids[b].astype(np.int64).tofile(os.path.join(d, "ids.i64"))
+    out["embed"][j].cpu().numpy().astype(np.int32).tofile(os.path.join(d, "exp_embed.i32"))
+    out["resid"][:, j].cpu().numpy().astype(np.int32).tofile(os.path.join(d, "exp_resid_out.i32"))
+    out["logits"][b].cpu().numpy().astype(np.int32).tofile(os.path.join(d, "exp_logits.i32"))
+    os.symlink(os.path.abspath(model_path), os.path.join(d, "model.bin"))
 
 
 def measured_traffic(kernel, config):
@@ -218,7 +309,11 @@ def main():
     ap.add_argument("--decode", action="store_true",
                     help="time KV-cached decoding instead: the configuration's sequences minus their last "
                          "--steps tokens as the prompt, then --steps single-token appends (one JSON line)")
+    ap.add_argument("--cpu-numpy-leg", nargs=2, metavar=("MODEL", "IDS"), help=argparse.SUPPRESS)
     args = ap.parse_args()
+    if args.cpu_numpy_leg:
+        numpy_leg_child(*args.cpu_numpy_leg)
+        return
     if args.copy_calibration:
         copy_calibration()
         return
@@ -282,10 +377,14 @@ def main():
     dom = max(ops, key=lambda k: per_kind[k]["ms_total"])
     t_dom = per_kind[dom]["ms_total"] * 1e-3 / args.steps           # seconds per step in this class
     n_dom = per_kind[dom]["launches"] / args.steps
-    mfma_ops_launch = ops[dom][1] / n_dom
+    alg_ops_launch = ops[dom][0] / n_dom                              # 2 M N K per launch
+    mfma_ops_launch = ops[dom][1] / n_dom                             # x limbs: int8 MFMA passes issued
     avg_launch_s = t_dom / n_dom
-    achieved = mfma_ops_launch / avg_launch_s
+    achieved = alg_ops_launch / avg_launch_s
     fwd_mfma_ops = sum(v[1] for v in ops.values())
+    # the forward's algorithmic ops: every projection and the head (2 M N K) plus attention's QK and
+    # PV over the causal triangle, 2 x 9 heads x 64 x T (T + 1) / 2 MACs x 2 per sequence per layer
+    fwd_alg_ops = sum(v[0] for v in ops.values()) + NL * B * 2 * 9 * 64 * T * (T + 1)
 
     # exactness of the timed workload: one more forward dumping the states of the sampled
     # sequences (and of sequence 0, which the CPU baseline checks), against the committed oracle
@@ -307,10 +406,22 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline:
+        host = host_cpu()
+        # the same sampled sequences on every leg: the first CPU_SEQS of the dumped ones
+        sample = [(b, j) for j, b in enumerate(dumped)][:CPU_SEQS]
+        legs = []
         if os.path.exists(REF_BIN) and T <= 512:
-            cpu = cpu_baseline_reference(model_path, ids_np, out)
+            cpu = cpu_baseline_reference(model_path, ids_np, out, sample)
         else:
             cpu = cpu_baseline_port(model_path, ids_np)
+        if os.path.exists(ORACLE_C) and T <= 512:
+            legs.append(cpu_leg_c_restatement(model_path, ids_np, out, sample, host["threads_used_all_core"]))
+        legs.append(cpu_leg_numpy(ids_np, sample, 1, model_path))
+        legs.append(cpu_leg_numpy(ids_np, sample, host["threads_used_all_core"], model_path))
+        cpu["host"] = host
+        cpu["legs"] = legs
+        cpu["note"] = ("every leg runs the same sampled sequences of the benchmark batch; sequences are "
+                       "independent, so the whole batch takes B / len(sample) times as long on one leg's cores")
 
     traffic = measured_traffic(dom, args.config)
     res = {
@@ -326,11 +437,19 @@ def main():
         "exact_sampled_sequences": exact,
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": achieved / 1e12, "peak": PEAK_INT8_OPS / 1e12,
                      "unit": "TFLOP/s", "frac": achieved / PEAK_INT8_OPS,
+                     "frac_algorithmic": achieved / PEAK_INT8_OPS,
                      "traffic": traffic["bytes"] if traffic else None,
                      "traffic_detail": traffic,
-                     "ops_per_launch_int8_mfma": mfma_ops_launch, "ops_per_launch_algorithmic": ops[dom][0] / n_dom,
+                     "ops_per_launch_algorithmic": alg_ops_launch,
+                     "limb_weighted": {"ops_per_launch_int8_mfma": mfma_ops_launch,
+                                       "achieved": mfma_ops_launch / avg_launch_s / 1e12,
+                                       "frac": mfma_ops_launch / avg_launch_s / PEAK_INT8_OPS,
+                                       "meaning": "int8 MFMA passes issued (one per activation limb) per second "
+                                                  "against the int8 peak: a busy measure, not the roofline"},
                      "avg_launch_ms": avg_launch_s * 1e3},
-        "forward_mfma_frac": fwd_mfma_ops / (elapsed / args.steps) / PEAK_INT8_OPS,
+        "forward_frac_algorithmic": fwd_alg_ops / (elapsed / args.steps) / PEAK_INT8_OPS,
+        "forward_ops_per_token_algorithmic": fwd_alg_ops / M,
+        "forward_mfma_frac_limb_weighted": fwd_mfma_ops / (elapsed / args.steps) / PEAK_INT8_OPS,
         "kernels_ms_per_step": {k: v["ms_total"] / args.steps for k, v in per_kind.items()},
         "cpu_baseline": cpu,
     }

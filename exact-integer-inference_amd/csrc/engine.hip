@@ -253,7 +253,7 @@ extern "C" int eii_model_load(const char* path, int device, eii_model** out) {
     if ((rc = narrow32(emb_m, (int32_t*)(ar.host.data() + o_embm), -(1 << 14), 1 << 14, "emb_m")) ||
         (rc = narrow32(esh, (int32_t*)(ar.host.data() + o_embsh), 1, 62, "embedding shift emb_n - 15")) ||
         (rc = narrow32(hsh, (int32_t*)(ar.host.data() + o_headsh), 1, 62, "head shift emb_n + f_y - 16")) ||
-        (rc = narrow32(fgq, (int32_t*)(ar.host.data() + o_fg), INT32_MIN + 1, INT32_MAX, "final gain")) ||
+        (rc = narrow32(fgq, (int32_t*)(ar.host.data() + o_fg), -32768, 32767, "final gain")) ||
         (rc = narrow32(expt, (int32_t*)(ar.host.data() + o_exp), 0, INT32_MAX, "exp table")) ||
         (rc = narrow32(rc_, (int32_t*)(ar.host.data() + o_rc), INT32_MIN, INT32_MAX, "rope cos")) ||
         (rc = narrow32(rs_, (int32_t*)(ar.host.data() + o_rs), INT32_MIN, INT32_MAX, "rope sin"))) {
@@ -311,8 +311,10 @@ extern "C" int eii_model_load(const char* path, int device, eii_model** out) {
     LayerOff& O = lo[l];
     O.ln1 = ar.take(4 * kD);
     O.ln2 = ar.take(4 * kD);
-    if ((rc = narrow32(ln1, (int32_t*)(ar.host.data() + O.ln1), INT32_MIN + 1, INT32_MAX, "ln1")) ||
-        (rc = narrow32(ln2, (int32_t*)(ar.host.data() + O.ln2), INT32_MIN + 1, INT32_MAX, "ln2"))) {
+    // RMSNorm gains are int16 (python/intref.py:126-130 quant_vec_int16); the forward's norm kernel
+    // relies on |3 gain| < 2^17
+    if ((rc = narrow32(ln1, (int32_t*)(ar.host.data() + O.ln1), -32768, 32767, "ln1")) ||
+        (rc = narrow32(ln2, (int32_t*)(ar.host.data() + O.ln2), -32768, 32767, "ln2"))) {
       delete M;
       return rc;
     }
@@ -570,7 +572,8 @@ int run_block(eii_model* m, int l, int32_t* x, int M, int nseq, int max_T, const
   uint8_t* h = (uint8_t*)m->h;
   {
     ProfScope ps(m, EII_K_NORM, s);
-    HIPCHK(rmsnorm(x, M, L.ln1, 21 + L.ln1_f - L.f[NORM1], L.bits[NORM1], h, tr ? tr->norm1_out : nullptr, s));
+    HIPCHK(rmsnorm(x, M, L.ln1, 21 + L.ln1_f - L.f[NORM1], L.bits[NORM1], h, tr ? tr->norm1_out : nullptr, s, false,
+                   tr ? tr->norm1_U : nullptr, tr ? tr->norm1_z : nullptr));
   }
   const int sh_q = 30 + L.f[QP] - L.f[QR], sh_k = 30 + L.f[KP] - L.f[KR];
   {
@@ -594,6 +597,11 @@ int run_block(eii_model* m, int l, int32_t* x, int M, int nseq, int max_T, const
     if (tr->q_rope) HIPCHK(copy_cols(tr->q_rope, kD, m->qkv, kQKVN, 0, kD, 2, M, s));
     if (tr->k_rope) HIPCHK(copy_cols(tr->k_rope, 192, m->qkv, kQKVN, kD, 192, 2, M, s));
     HIPCHK(build_vt(m->qkv, M, m->vt, s));
+    if (tr->attn_score || tr->attn_prob) {   // both written together: the probabilities re-read the scores
+      if (!tr->attn_score || !tr->attn_prob) return fail(EII_E_ARG, "trace: attn_score and attn_prob go together");
+      HIPCHK(attn_trace(m->qkv, nseq, max_T, m->exp_tab, L.f[QR] + L.f[KR] + 3 - kFScore, tr->attn_score,
+                        tr->attn_prob, s));
+    }
   }
   const int cb = L.bits[CTX] / 8;
   {
@@ -613,6 +621,14 @@ int run_block(eii_model* m, int l, int32_t* x, int M, int nseq, int max_T, const
     }
     HIPCHK(attention(a, s));
   }
+  // traces: RS(acc m, n + f_c - 15) before the saturating add, from the exact int64 accumulators
+  auto res_update = [&](const Mat& W, const void* planes, int planes_n, int64_t* out) -> int {
+    HIPCHK(gemm_i64_anyk((const uint8_t*)planes, planes_n, W.Wf, W.wsum, M, W.N, W.K, out, s));
+    HIPCHK(requant_i64(out, M, W.N, W.mult, W.shift, 64, out, s));
+    return EII_OK;
+  };
+  int rc;
+  if (tr && tr->o_res && (rc = res_update(L.o, m->ctx, cb, tr->o_res))) return rc;
   {
     ProfScope ps(m, EII_K_GEMM_O, s);
     HIPCHK(gemm(gemm_args(L.o, m->ctx, M, x, 32), cb, EPI_RESID, s));
@@ -621,7 +637,8 @@ int run_block(eii_model* m, int l, int32_t* x, int M, int nseq, int max_T, const
   const int h2b = L.bits[NORM2] / 8;
   {
     ProfScope ps(m, EII_K_NORM, s);
-    HIPCHK(rmsnorm(x, M, L.ln2, 21 + L.ln2_f - L.f[NORM2], L.bits[NORM2], h, tr ? tr->norm2_out : nullptr, s));
+    HIPCHK(rmsnorm(x, M, L.ln2, 21 + L.ln2_f - L.f[NORM2], L.bits[NORM2], h, tr ? tr->norm2_out : nullptr, s, false,
+                   tr ? tr->norm2_U : nullptr, tr ? tr->norm2_z : nullptr));
   }
   const int gb = L.bits[GATED] / 8;
   const int sh_s = L.f[SILU] + L.f[UP] - L.f_m;
@@ -642,7 +659,8 @@ int run_block(eii_model* m, int l, int32_t* x, int M, int nseq, int max_T, const
     if (tr->up_proj)
       HIPCHK(hipMemcpy2DAsync(tr->up_proj, 64, (const uint8_t*)m->gu + 64, 128, 64, (size_t)M * 48,
                               hipMemcpyDeviceToDevice, s));
-    HIPCHK(silu_gate(m->gu, M, L.silu, sh_s, L.bits[GATED], (uint8_t*)m->gated, tr->mlp_gated, s));
+    HIPCHK(silu_gate(m->gu, M, L.silu, sh_s, L.bits[GATED], (uint8_t*)m->gated, tr->mlp_gated, s, tr->silu_gate));
+    if (tr->down_res && (rc = res_update(L.down, m->gated, gb, tr->down_res))) return rc;
   }
   {
     ProfScope ps(m, EII_K_GEMM_DOWN, s);
@@ -904,13 +922,18 @@ extern "C" int eii_weight_colsum(const int8_t* W, int N, int K, int32_t* wsum, v
   return EII_OK;
 }
 
+// K is zero-padded to a multiple of 64 for the GEMM (zero weight columns add nothing); every limb
+// partial sum stays inside int32 while 128 * 127 * K < 2^31
+constexpr int kMaxGemmK = 131072;
 static int check_gemm_args(const void* A, int a_bits, const int8_t* W, int M, int N, int K) {
   if (!A || !W || M <= 0 || N <= 0 || K <= 0) return fail(EII_E_ARG, "bad gemm arguments");
-  if (a_bits != 16 && a_bits != 32) return fail(EII_E_ARG, "a_bits must be 16 or 32");
-  if (K != 64 && K != 128 && K != 576 && K != 1536) return fail(EII_E_ARG, "K must be 64, 128, 576 or 1536");
-  if (K > 65536) return fail(EII_E_BOUND, "K above 65536 could overflow a limb partial sum");
+  if (a_bits != 8 && a_bits != 16 && a_bits != 32) return fail(EII_E_ARG, "a_bits must be 8, 16 or 32");
+  if (K > kMaxGemmK) return fail(EII_E_BOUND, "K above 131072 could overflow a limb partial sum");
+  if ((size_t)M * padded_k(K) > ((size_t)1 << 31)) return fail(EII_E_ARG, "M * K above 2^31");
   return EII_OK;
 }
+// limb planes of an a_bits activation: 8- and 16-bit values travel as 2 planes, 32-bit as 4
+static int limb_planes(int a_bits) { return a_bits == 32 ? 4 : 2; }
 
 // Staging memory of the operator entry points (A split into K-blocked limb planes, W in fragment
 // order, column sums, requantization coefficients, V^T planes): one block per device, kept for
@@ -971,18 +994,25 @@ class Staging {
 };
 
 static size_t operand_bytes(int a_bits, int M, int N, int K) {
-  return Staging::align((size_t)M * K * (a_bits / 8)) + Staging::align(swizzled_bytes(N, K));
+  const int Kp = padded_k(K);
+  return Staging::align((size_t)M * Kp * limb_planes(a_bits)) + Staging::align(swizzled_bytes(N, Kp));
 }
 
-// A [M, K] -> K-blocked limb planes, row-major W [N, K] -> fragment order, in the staging block.
-static int stage_operands(const void* A, int a_bits, const int8_t* W, int M, int N, int K, Staging& st,
-                          uint8_t*& planes, int8_t*& wf, hipStream_t s) {
-  planes = st.carve<uint8_t>((size_t)M * K * (a_bits / 8));
-  wf = st.carve<int8_t>(swizzled_bytes(N, K));
+// A [M, K] -> K-blocked limb planes, row-major W [N, K] -> fragment order, both over K padded to a
+// multiple of 64, at the given device addresses (planes then wf)
+static int stage_operands_at(const void* A, int a_bits, const int8_t* W, int M, int N, int K, uint8_t* planes,
+                             int8_t* wf, hipStream_t s) {
   hipError_t e = split_limbs(A, a_bits / 8, M, K, planes, s);
-  if (e == hipSuccess) e = swizzle_weights(W, N, K, wf, s);
+  if (e == hipSuccess) e = swizzle_weights(W, N, K, wf, s, padded_k(K));
   if (e != hipSuccess) return fail(EII_E_DEVICE, std::string("operand staging: ") + hipGetErrorString(e));
   return EII_OK;
+}
+
+static int stage_operands(const void* A, int a_bits, const int8_t* W, int M, int N, int K, Staging& st,
+                          uint8_t*& planes, int8_t*& wf, hipStream_t s) {
+  planes = st.carve<uint8_t>((size_t)M * padded_k(K) * limb_planes(a_bits));
+  wf = st.carve<int8_t>(swizzled_bytes(N, padded_k(K)));
+  return stage_operands_at(A, a_bits, W, M, N, K, planes, wf, s);
 }
 
 static int gemm_i8_staged(const void* A, int a_bits, const int8_t* W, const int32_t* wsum, int M, int N, int K,
@@ -991,8 +1021,7 @@ static int gemm_i8_staged(const void* A, int a_bits, const int8_t* W, const int3
   int8_t* wf;
   int rc;
   if ((rc = stage_operands(A, a_bits, W, M, N, K, st, planes, wf, s))) return rc;
-  GemmArgs g{planes, wf, M, N, K, (size_t)M * K, wsum, nullptr, nullptr, acc, 64, nullptr};
-  hipError_t e = gemm(g, a_bits / 8, EPI_I64, s);
+  const hipError_t e = gemm_i64_anyk(planes, limb_planes(a_bits), wf, wsum, M, N, padded_k(K), acc, s);
   if (e != hipSuccess) return fail(EII_E_DEVICE, std::string("eii_gemm_i8: ") + hipGetErrorString(e));
   return EII_OK;
 }
@@ -1024,6 +1053,8 @@ extern "C" int eii_gemm_i8(const void* A, int a_bits, const int8_t* W, int M, in
   return gemm_i8_staged(A, a_bits, W, ws, M, N, K, acc, st, s);
 }
 
+// The requantization runs on the exact int64 accumulators, in int64 as python/intref.py:189 does,
+// so any int32 multiplier and shift behave as there (the reference asserts |acc| max m < 2^63).
 extern "C" int eii_linear(const void* A, int a_bits, const int8_t* W, const int32_t* wsum, const int32_t* mult,
                           const int32_t* shift, int M, int N, int K, int out_bits, void* out, void* stream) {
   int rc;
@@ -1033,18 +1064,11 @@ extern "C" int eii_linear(const void* A, int a_bits, const int8_t* W, const int3
   if (N % 4) return fail(EII_E_ARG, "N must be a multiple of 4");
   hipStream_t s = (hipStream_t)stream;
   Staging st;
-  if ((rc = st.take(operand_bytes(a_bits, M, N, K) + Staging::align((size_t)N * sizeof(double2)), s))) return rc;
-  uint8_t* planes;
-  int8_t* wf;
-  if ((rc = stage_operands(A, a_bits, W, M, N, K, st, planes, wf, s))) return rc;
-  GemmArgs g{planes, wf, M, N, K, (size_t)M * K, wsum, mult, shift, out, out_bits, nullptr};
-  hipError_t e = hipSuccess;
-  if (a_bits == 16) {
-    double2* coef = st.carve<double2>((size_t)N * sizeof(double2));
-    e = gemm_coef(mult, shift, wsum, N, coef, s);
-    g.coef = coef;
-  }
-  if (e == hipSuccess) e = gemm(g, a_bits / 8, out_bits == 16 ? EPI_REQ16 : EPI_REQ32, s);
+  const size_t acc_bytes = (size_t)M * N * 8;
+  if ((rc = st.take(operand_bytes(a_bits, M, N, K) + Staging::align(acc_bytes), s))) return rc;
+  int64_t* acc = st.carve<int64_t>(acc_bytes);
+  if ((rc = gemm_i8_staged(A, a_bits, W, wsum, M, N, K, acc, st, s))) return rc;
+  const hipError_t e = requant_i64(acc, M, N, mult, shift, out_bits, out, s);
   if (e != hipSuccess) return fail(EII_E_DEVICE, std::string("eii_linear: ") + hipGetErrorString(e));
   return EII_OK;
 }
@@ -1109,7 +1133,8 @@ extern "C" int eii_rmsnorm(const int32_t* x, int M, const int32_t* gain, int f_g
   if (out_bits != 16 && out_bits != 32) return fail(EII_E_ARG, "out_bits must be 16 or 32");
   int rc;
   if ((rc = check_scalar_shift(21 + f_gain - f_out, "norm"))) return rc;
-  HIPCHK(rmsnorm(x, M, gain, 21 + f_gain - f_out, out_bits, nullptr, out, (hipStream_t)stream));
+  // gains anywhere in int32: the general int64 path
+  HIPCHK(rmsnorm(x, M, gain, 21 + f_gain - f_out, out_bits, nullptr, out, (hipStream_t)stream, true));
   return EII_OK;
 }
 

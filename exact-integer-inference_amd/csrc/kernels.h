@@ -32,7 +32,8 @@ __host__ __device__ inline size_t plane_offset(size_t m, size_t k, size_t M) {
 // [ceil(N / 32)][K / 32][64][16] (lane 32 h + c: row 32 b + c, columns 16 h .. 16 h + 15 of
 // the slice); rows past N are zero.
 inline size_t swizzled_bytes(int N, int K) { return (size_t)((N + 31) / 32) * 32 * K; }
-hipError_t swizzle_weights(const int8_t* W, int N, int K, int8_t* Wf, hipStream_t s);
+// W [N, K] row-major (any K) -> fragment order over Kp >= K columns (zero past K), Kp % 32 == 0
+hipError_t swizzle_weights(const int8_t* W, int N, int K, int8_t* Wf, hipStream_t s, int Kp = 0);
 
 struct GemmArgs {
   const void* A;          // limb planes of the [M, K] activations, 2 (16-bit) or 4 (32-bit) planes
@@ -59,6 +60,12 @@ struct GemmArgs {
   // EPI_QKV: also write v as the key-contiguous V^T limb planes described below, or null
   uint8_t* vt = nullptr;
   int vt_stride = 0;
+  // K of the whole fragment-ordered weight matrix when this launch covers a range of its K blocks
+  // (W and A then point at the first block of the range); 0 = K
+  int w_ld = 0;
+  // EPI_I64 only: add the accumulators to the int64 values already in out (K-range passes after
+  // the first); wsum may be null, meaning no limb bias term (the first pass adds it for all of K)
+  bool accumulate = false;
 };
 
 // V^T limb planes for attention: plane 0 = low bytes - 128, plane 1 = signed high bytes of v;
@@ -70,6 +77,17 @@ inline size_t vt_bytes(int M) { return (size_t)2 * 192 * vt_stride_for(M); }
 hipError_t build_vt(const int16_t* qkv, int M, uint8_t* vt, hipStream_t s);
 
 hipError_t gemm(const GemmArgs& a, int a_bytes, int epi, hipStream_t s);
+// Exact int64 out [M, N] = A W^T for any K: A as limb planes of K rounded up to a multiple of 64
+// (a_bytes 2 or 4), W in fragment order over the same padded K (zero columns past K), wsum [N];
+// the K blocks run in passes of the GEMM's compiled K-block counts, accumulated in out.
+hipError_t gemm_i64_anyk(const uint8_t* planes, int a_bytes, const int8_t* Wf, const int32_t* wsum, int M, int N,
+                         int Kp, int64_t* out, hipStream_t s);
+// out [M, N] (int16, int32 or int64 by out_bits; 64 = no saturation) = SAT(RS(acc * mult[n], shift[n]), out_bits)
+// from exact int64 (in place when out == acc)
+// accumulators (python/intref.py:189), in int64 as the reference
+hipError_t requant_i64(const int64_t* acc, int M, int N, const int32_t* mult, const int32_t* shift, int out_bits,
+                       void* out, hipStream_t s);
+inline int padded_k(int K) { return (K + 63) / 64 * 64; }
 hipError_t weight_colsum(const int8_t* W, int N, int K, int32_t* wsum, hipStream_t s);
 hipError_t gemm_coef(const int32_t* mult, const int32_t* shift, const int32_t* wsum, int N, double2* coef,
                      hipStream_t s);
@@ -79,12 +97,17 @@ hipError_t embed(const int64_t* ids, int M, const int8_t* emb_q, const int32_t* 
                  const int32_t* emb_sh, int32_t* x, int* flag, hipStream_t s);
 
 // out = SAT(RS(3 * RS(x * U, 16) * gain, sh_out), bits_out) as limb planes (bits/8 planes of
-// M x 576, K-blocked) and/or plain int16/int32 [M, 576] (either pointer may be null)
+// M x 576, K-blocked) and/or plain int16/int32 [M, 576] (either pointer may be null).  Gains
+// must be int16 unless wide_gain (any int32 gain, general int64 path); u_out int32 [M] and z_out
+// int32 [M, 576] (nullable) receive the norm's U and z = RS(x U, 16).
 hipError_t rmsnorm(const int32_t* x, int M, const int32_t* gain, int sh_out, int bits_out,
-                   uint8_t* planes, void* plain, hipStream_t s);
+                   uint8_t* planes, void* plain, hipStream_t s, bool wide_gain = false,
+                   int32_t* u_out = nullptr, int32_t* z_out = nullptr);
 
-// plain [M, K] int16 (a_bytes 2) or int32 (a_bytes 4), K % 64 == 0 -> K-blocked limb planes
-hipError_t split_limbs(const void* a, int a_bytes, int M, int K, uint8_t* planes, hipStream_t s);
+// plain [M, K] int8 (src_bytes 1), int16 (2) or int32 (4) -> K-blocked limb planes over K rounded
+// up to a multiple of 64 (padded_k; the columns past K hold 0): 2 planes for 8/16-bit values, 4 for
+// 32-bit ones
+hipError_t split_limbs(const void* a, int src_bytes, int M, int K, uint8_t* planes, hipStream_t s);
 
 // In-place rotate-half RoPE on the q (cols 0..575) and k (cols 576..767) parts of qkv [M, 960]
 hipError_t rope(int16_t* qkv, int M, const int32_t* pos, const int32_t* cosT, const int32_t* sinT,
@@ -92,8 +115,12 @@ hipError_t rope(int16_t* qkv, int M, const int32_t* pos, const int32_t* cosT, co
 
 // gated[m, j] = SAT(RS(silu[gate + 32768] * up, sh), bits) with gu rows holding [gate 32 | up 32]
 // blocks: gate j at column 64 (j / 32) + j % 32, up j 32 columns further
+// sg_out int32 [M, 1536] (nullable, traces): the table values silu[gate + 32768]
 hipError_t silu_gate(const int16_t* gu, int M, const int32_t* silu, int sh, int bits,
-                     uint8_t* planes, void* plain, hipStream_t s);
+                     uint8_t* planes, void* plain, hipStream_t s, int32_t* sg_out = nullptr);
+// Trace of attention's scores and probabilities for B sequences of T rows each (see kernels.hip)
+hipError_t attn_trace(const int16_t* qkv, int B, int T, const int32_t* exp_tab, int shift_s, int16_t* score_out,
+                      int32_t* prob_out, hipStream_t s);
 
 struct AttnArgs {
   const int16_t* qkv;      // [M, 960]: q rope | k rope (v is read from vt)

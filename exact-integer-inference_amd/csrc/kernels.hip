@@ -187,7 +187,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
       // this lane's B fragments: weight rows n0 + 64 wn + 32 tn + 0..31, the lane's 16 bytes of
       // each 32-column K slice
       const int nb32 = min((nb * C::BN + wn * C::WN + 32 * tn) >> 5, nb32_last);
-      w_src[tn] = g.W + (size_t)nb32 * (g.K / 32) * 1024 + lane * 16;
+      w_src[tn] = g.W + (size_t)nb32 * ((g.w_ld ? g.w_ld : g.K) / 32) * 1024 + lane * 16;
     }
   };
   // The pointers advance by one K block per load.  The increment goes through an empty asm so
@@ -294,7 +294,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
       for (int tn = 0; tn < C::TN; ++tn) {
         const int n = n0 + cw + 32 * tn;
         if (n >= g.N) continue;
-        const int32_t ws = (AW == 4 || EPI == EPI_I64) ? g.wsum[n] : 0;
+        const int32_t ws = (AW == 4 || EPI == EPI_I64) && g.wsum ? g.wsum[n] : 0;
         int32_t mu = 0, sh = 1;
         double2 k = make_double2(0.0, 0.0);
         if constexpr (AW == 4 && EPI != EPI_I64) { mu = g.mult[n]; sh = g.shift[n]; }
@@ -303,9 +303,18 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
 #pragma unroll
         for (int tm = 0; tm < C::TM; ++tm) {
           if constexpr (EPI == EPI_I64) {
+            if (g.accumulate) {
 #pragma unroll
-            for (int e = 0; e < 16; ++e)
-              if (live(tm, e)) __builtin_nontemporal_store(acc64(tm, tn, e, ws), at(tb, N, lane_b, tm, e, 32 * tn));
+              for (int e = 0; e < 16; ++e)
+                if (live(tm, e)) {
+                  OT* p = at(tb, N, lane_b, tm, e, 32 * tn);
+                  *p = *p + acc64(tm, tn, e, ws);
+                }
+            } else {
+#pragma unroll
+              for (int e = 0; e < 16; ++e)
+                if (live(tm, e)) __builtin_nontemporal_store(acc64(tm, tn, e, ws), at(tb, N, lane_b, tm, e, 32 * tn));
+            }
             continue;
           }
           // residual epilogue: the loads of 8 rows issue together, then their updates
@@ -647,29 +656,57 @@ hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
   return launch_gemm_cfg<AW, EPI, false>(a, s);
 }
 
-template <int W>
-__global__ __launch_bounds__(256) void split_kernel(const void* a, int M, int K, uint8_t* planes) {
-  const size_t i = ((size_t)blockIdx.x * 256 + threadIdx.x) * 4;   // 4 consecutive elements of a row
-  const size_t n = (size_t)M * K;
-  if (i >= n) return;
-  const size_t m = i / K, k = i % K;
+// thread = 4 consecutive elements (k = 4 i .. 4 i + 3) of one row of the padded [M, Kp] operand
+template <int SW, int W>
+__global__ __launch_bounds__(256) void split_kernel(const void* a, int M, int K, int Kp, uint8_t* planes) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x, n4 = (size_t)M * (Kp / 4);
+  if (i >= n4) return;
+  const size_t m = i / (Kp / 4), k = (i % (Kp / 4)) * 4;
   int32_t v[4];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) v[e] = W == 2 ? ((const int16_t*)a)[i + e] : ((const int32_t*)a)[i + e];
+  for (int e = 0; e < 4; ++e) {
+    const size_t j = m * K + k + e;
+    v[e] = k + e >= (size_t)K ? 0
+           : SW == 1        ? (int32_t)((const int8_t*)a)[j]
+           : SW == 2        ? (int32_t)((const int16_t*)a)[j]
+                            : ((const int32_t*)a)[j];
+  }
+  const size_t n = (size_t)M * Kp;
 #pragma unroll
   for (int l = 0; l < W; ++l) *(uint32_t*)(planes + l * n + plane_offset(m, k, M)) = limb_word(v, l, W);
 }
 
-// Weights [N, K] row-major -> fragment order (kernels.h swizzle_weights): thread = 16 bytes
-__global__ __launch_bounds__(256) void swizzle_kernel(const int8_t* W, int N, int K, int8_t* Wf) {
-  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x, ks = K / 32;
+// Weights [N, K] row-major -> fragment order over Kp columns (kernels.h swizzle_weights): thread =
+// 16 bytes; columns past K and rows past N are zero
+__global__ __launch_bounds__(256) void swizzle_kernel(const int8_t* W, int N, int K, int Kp, int8_t* Wf) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x, ks = Kp / 32;
   if (i >= (size_t)((N + 31) / 32) * ks * 64) return;
   const int lane = (int)(i & 63);
   const size_t kc = (i >> 6) % ks, nb = (i >> 6) / ks;
   const size_t n = nb * 32 + (lane & 31), k = kc * 32 + 16 * (lane >> 5);
   uint4 v = make_uint4(0, 0, 0, 0);
-  if (n < (size_t)N) v = *(const uint4*)(W + n * K + k);
+  if (n < (size_t)N) {
+    const int8_t* src = W + n * K + k;
+    if (K % 16 == 0 && k + 16 <= (size_t)K) {
+      v = *(const uint4*)src;
+    } else {
+      uint32_t w[4] = {0, 0, 0, 0};
+      for (int b = 0; b < 16; ++b)
+        if (k + b < (size_t)K) w[b >> 2] |= (uint32_t)(uint8_t)src[b] << (8 * (b & 3));
+      v = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+  }
   *(uint4*)(Wf + i * 16) = v;
+}
+
+// out = SAT(RS(acc * mult[n], shift[n]), out_bits): thread = one element
+template <typename OT>
+__global__ __launch_bounds__(256) void requant_kernel(const int64_t* acc, int M, int N, const int32_t* mult,
+                                                      const int32_t* shift, int out_bits, OT* out) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (size_t)M * N) return;
+  const int n = (int)(i % N);
+  out[i] = (OT)sat(rs(acc[i] * (int64_t)mult[n], shift[n]), out_bits);
 }
 
 __global__ __launch_bounds__(256) void coef_kernel(const int32_t* mult, const int32_t* shift, const int32_t* wsum,
@@ -714,11 +751,15 @@ __global__ __launch_bounds__(256) void embed_kernel(const int64_t* ids, int M, c
 // One wave per row; lane j holds elements j, j+64, ..., j+512.  Every product is a 32 x 32 -> 64
 // bit multiply-add: the squares through the 16-bit halves of x (python/intref.py:170-172),
 // z = RS(x U, 16) with U < 2^29 and |z| <= 2^24 (|x U| <= 2^40 since |x| <= sqrt(S)), then
-// 3 z gain with |3 z gain| < 2^41.  For output shifts in [10, 40] the shifted value fits int32
-// and saturates with one clamp; other shifts take the general int64 path.
-template <int OB>
+// 3 z gain.  With int16 gains (the model's, python/intref.py:126-130) |3 z gain| < 2^41, so for
+// output shifts in [10, 40] the shifted value fits int32 and saturates with one clamp; other
+// shifts take the general int64 path.  WIDE: gains anywhere in int32 (the operator entry point),
+// 3 gain and the product formed in int64 (|3 z gain| < 2^58) and saturated before narrowing.
+// u_out / z_out (trace only, nullable): U per row and z per element (python/intref.py:183).
+template <int OB, bool WIDE>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const int32_t* x, int M, const int32_t* gain,
-                                                      int sh_out, int bits_out, uint8_t* planes, void* plain) {
+                                                      int sh_out, int bits_out, uint8_t* planes, void* plain,
+                                                      int32_t* u_out, int32_t* z_out) {
   // 16 lanes per row, 4 rows per wave: lane c of a row holds columns 64 k + 4 c .. + 3, k = 0..8,
   // so loads are 16 bytes, the limb bytes of 4 columns leave as one dword, the row sums reduce in
   // 4 steps inside the 16-lane group and each lane evaluates its own row's U
@@ -740,7 +781,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const int32_t* x, int M, c
       const int32_t hi = e[r] >> 16, lo = e[r] & 0xFFFF;
       A += (int64_t)hi * hi; B += (int64_t)hi * lo; Cs += (int64_t)lo * lo;
     }
-    g3[k].x *= 3; g3[k].y *= 3; g3[k].z *= 3; g3[k].w *= 3;
+    if constexpr (!WIDE) { g3[k].x *= 3; g3[k].y *= 3; g3[k].z *= 3; g3[k].w *= 3; }
   }
 #pragma unroll
   for (int o = 8; o > 0; o >>= 1) {
@@ -748,13 +789,17 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const int32_t* x, int M, c
   }
   const int32_t U = (int32_t)norm_U(norm_total(A, B, Cs));   // < 2^29
   if (row >= M) return;
+  if (u_out && c == 0) u_out[row] = U;
   const size_t pl = (size_t)M * kD, m64 = (size_t)M * 64;
   // the output shift is uniform: one copy of the loop per path
   auto body = [&](auto FAST) __attribute__((always_inline)) {
     const int64_t rnd = (int64_t)1 << (min(max(sh_out, 10), 40) - 1);
+    auto zof = [&](int32_t xv) -> int32_t { return (int32_t)(((int64_t)xv * U + 32768) >> 16); };
     auto norm1 = [&](int32_t xv, int32_t gv) -> int32_t {
-      const int32_t z = (int32_t)(((int64_t)xv * U + 32768) >> 16);
-      if constexpr (decltype(FAST)::value) {
+      const int32_t z = zof(xv);
+      if constexpr (WIDE) {
+        return (int32_t)sat(rs((int64_t)z * (3 * (int64_t)gv), sh_out), bits_out);
+      } else if constexpr (decltype(FAST)::value) {
         const int32_t q = (int32_t)(((int64_t)z * gv + rnd) >> sh_out);
         return OB == 2 ? min(max(q, -32768), 32767) : q;
       } else {
@@ -775,9 +820,11 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const int32_t* x, int M, c
         if constexpr (OB == 2) *(uint2*)((int16_t*)plain + e) = make_uint2(pack16(o[0], o[1]), pack16(o[2], o[3]));
         else *(int4*)((int32_t*)plain + e) = make_int4(o[0], o[1], o[2], o[3]);
       }
+      if (z_out)
+        *(int4*)(z_out + (size_t)row * kD + 64 * k + 4 * c) = make_int4(zof(v[k].x), zof(v[k].y), zof(v[k].z), zof(v[k].w));
     }
   };
-  if (sh_out >= 10 && sh_out <= 40) body(std::true_type{});
+  if (!WIDE && sh_out >= 10 && sh_out <= 40) body(std::true_type{});
   else body(std::false_type{});
 }
 
@@ -801,7 +848,7 @@ __global__ __launch_bounds__(256) void rope_kernel(int16_t* qkv, int M, const in
 // ------------------------------------------------------------------------------ silu gate
 template <int OB>
 __global__ __launch_bounds__(256) void silu_kernel(const int16_t* gu, int M, const int32_t* silu,
-                                                   int sh, int bits, uint8_t* planes, void* plain) {
+                                                   int sh, int bits, uint8_t* planes, void* plain, int32_t* sg_out) {
   const size_t t = (size_t)blockIdx.x * 256 + threadIdx.x;
   if (t >= (size_t)M * kDFF) return;
   const size_t row = t / kDFF, j = t % kDFF;
@@ -810,6 +857,7 @@ __global__ __launch_bounds__(256) void silu_kernel(const int16_t* gu, int M, con
   const int g = gu[gi];
   const int64_t u = gu[gi + 32];
   const int32_t o = (int32_t)sat(rs((int64_t)silu[g + 32768] * u, sh), bits);
+  if (sg_out) sg_out[t] = silu[g + 32768];
   if (planes) {
 #pragma unroll
     for (int l = 0; l < OB; ++l) planes[l * (size_t)M * kDFF + plane_offset(row, j, M)] = (uint8_t)limb_byte(o, l, OB);
@@ -1227,8 +1275,13 @@ __global__ __launch_bounds__(192) __attribute__((amdgpu_waves_per_eu(2))) void a
 // wave's first value chunk is loaded before the reductions, so its latency hides behind them.
 // No key is masked: every cached key precedes the query.
 constexpr int kDecodeMaxKeys = 8192;   // scores of 3 heads x 8192 keys: 48 KB of LDS
+// LDS: exp table [1537] + 3 pad ints (the end stays 16-byte aligned), the row maxima [3 NW] in an
+// even count of ints (so the int64 arrays after them are 8-byte aligned for every NW), the exp sums
+// [3 NW] and partial context sums [3 NW][64] as int64, the scores of 3 heads as int16
+__host__ __device__ inline int attn_decode_nmax(int NW) { return (3 * NW + 1) & ~1; }
 __host__ __device__ inline size_t attn_decode_lds(int L, int NW) {
-  return (size_t)(kDMax + 1 + 3) * 4 + (size_t)3 * NW * (4 + 8 + 64 * 8) + (size_t)3 * ((L + 63) & ~63) * 2;
+  return (size_t)(kDMax + 1 + 3) * 4 + (size_t)attn_decode_nmax(NW) * 4 + (size_t)3 * NW * (8 + 64 * 8) +
+         (size_t)3 * ((L + 63) & ~63) * 2;
 }
 
 template <int OB, int NW>
@@ -1238,8 +1291,8 @@ __global__ __launch_bounds__(64 * 3 * NW) void attn_decode_kernel(AttnArgs a) {
   const int seq = blockIdx.x, kvg = blockIdx.y, hh = 3 * kvg + hq;
   const int L = a.kv_len, Lp = (L + 63) & ~63;
   int32_t* etab = dsm;                                          // [1537] (+3 pad)
-  int32_t* smax = dsm + kDMax + 1 + 3;                          // [12]
-  int64_t* sz = (int64_t*)(smax + 3 * NW);                      // [12]
+  int32_t* smax = dsm + kDMax + 1 + 3;                          // [3 NW], padded to an even count
+  int64_t* sz = (int64_t*)(smax + attn_decode_nmax(NW));        // [3 NW]
   int64_t* spart = sz + 3 * NW;                                 // [12][64]
   int16_t* sc = (int16_t*)(spart + 3 * NW * 64) + (size_t)hq * Lp;
   for (int i = tid; i <= kDMax; i += 64 * 3 * NW) etab[i] = a.exp_tab[i];
@@ -1404,25 +1457,67 @@ hipError_t embed(const int64_t* ids, int M, const int8_t* emb_q, const int32_t* 
 }
 
 hipError_t rmsnorm(const int32_t* x, int M, const int32_t* gain, int sh_out, int bits_out, uint8_t* planes,
-                   void* plain, hipStream_t s) {
+                   void* plain, hipStream_t s, bool wide_gain, int32_t* u_out, int32_t* z_out) {
   dim3 grid((M + 15) / 16);
-  if (bits_out == 16) hipLaunchKernelGGL(rmsnorm_kernel<2>, grid, dim3(256), 0, s, x, M, gain, sh_out, bits_out, planes, plain);
-  else hipLaunchKernelGGL(rmsnorm_kernel<4>, grid, dim3(256), 0, s, x, M, gain, sh_out, bits_out, planes, plain);
+  if (bits_out != 16 && bits_out != 32) return hipErrorInvalidValue;
+#define EII_NORM(OB, W) hipLaunchKernelGGL((rmsnorm_kernel<OB, W>), grid, dim3(256), 0, s, x, M, gain, sh_out, bits_out, \
+                                           planes, plain, u_out, z_out)
+  if (wide_gain) {
+    if (bits_out == 16) EII_NORM(2, true);
+    else EII_NORM(4, true);
+  } else {
+    if (bits_out == 16) EII_NORM(2, false);
+    else EII_NORM(4, false);
+  }
+#undef EII_NORM
   return hipGetLastError();
 }
 
-hipError_t split_limbs(const void* a, int a_bytes, int M, int K, uint8_t* planes, hipStream_t s) {
-  if (K % 64 != 0) return hipErrorInvalidValue;
-  dim3 grid(blocks_for((size_t)M * K / 4));
-  if (a_bytes == 2) hipLaunchKernelGGL(split_kernel<2>, grid, dim3(256), 0, s, a, M, K, planes);
-  else hipLaunchKernelGGL(split_kernel<4>, grid, dim3(256), 0, s, a, M, K, planes);
+hipError_t split_limbs(const void* a, int src_bytes, int M, int K, uint8_t* planes, hipStream_t s) {
+  if (M <= 0 || K <= 0) return hipErrorInvalidValue;
+  const int Kp = padded_k(K);
+  dim3 grid(blocks_for((size_t)M * Kp / 4));
+  if (src_bytes == 1) hipLaunchKernelGGL((split_kernel<1, 2>), grid, dim3(256), 0, s, a, M, K, Kp, planes);
+  else if (src_bytes == 2) hipLaunchKernelGGL((split_kernel<2, 2>), grid, dim3(256), 0, s, a, M, K, Kp, planes);
+  else if (src_bytes == 4) hipLaunchKernelGGL((split_kernel<4, 4>), grid, dim3(256), 0, s, a, M, K, Kp, planes);
+  else return hipErrorInvalidValue;
   return hipGetLastError();
 }
 
-hipError_t swizzle_weights(const int8_t* W, int N, int K, int8_t* Wf, hipStream_t s) {
-  if (K % 32 != 0 || N <= 0) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(swizzle_kernel, dim3(blocks_for((size_t)((N + 31) / 32) * (K / 32) * 64)), dim3(256), 0, s, W, N,
-                     K, Wf);
+hipError_t swizzle_weights(const int8_t* W, int N, int K, int8_t* Wf, hipStream_t s, int Kp) {
+  if (Kp == 0) Kp = K;
+  if (Kp % 32 != 0 || Kp < K || N <= 0 || K <= 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(swizzle_kernel, dim3(blocks_for((size_t)((N + 31) / 32) * (Kp / 32) * 64)), dim3(256), 0, s, W,
+                     N, K, Kp, Wf);
+  return hipGetLastError();
+}
+
+hipError_t gemm_i64_anyk(const uint8_t* planes, int a_bytes, const int8_t* Wf, const int32_t* wsum, int M, int N,
+                         int Kp, int64_t* out, hipStream_t s) {
+  if (Kp <= 0 || Kp % kBK != 0) return hipErrorInvalidValue;
+  // passes over ranges of the K blocks, each a compiled K-block count (24, 9, 2 or 1), largest first
+  int b0 = 0;
+  const int nkb = Kp / kBK;
+  while (b0 < nkb) {
+    const int left = nkb - b0, nb = left >= 24 ? 24 : left >= 9 ? 9 : left >= 2 ? 2 : 1;
+    GemmArgs g{planes + (size_t)b0 * M * 64, Wf + (size_t)b0 * 2 * 1024, M, N, nb * kBK, (size_t)M * Kp,
+               b0 == 0 ? wsum : nullptr, nullptr, nullptr, out, 64, nullptr};
+    g.w_ld = Kp;
+    g.accumulate = b0 > 0;
+    const hipError_t e = gemm(g, a_bytes, EPI_I64, s);
+    if (e != hipSuccess) return e;
+    b0 += nb;
+  }
+  return hipSuccess;
+}
+
+hipError_t requant_i64(const int64_t* acc, int M, int N, const int32_t* mult, const int32_t* shift, int out_bits,
+                       void* out, hipStream_t s) {
+  const dim3 grid(blocks_for((size_t)M * N));
+  if (out_bits == 16) hipLaunchKernelGGL(requant_kernel<int16_t>, grid, dim3(256), 0, s, acc, M, N, mult, shift, 16, (int16_t*)out);
+  else if (out_bits == 32) hipLaunchKernelGGL(requant_kernel<int32_t>, grid, dim3(256), 0, s, acc, M, N, mult, shift, 32, (int32_t*)out);
+  else if (out_bits == 64) hipLaunchKernelGGL(requant_kernel<int64_t>, grid, dim3(256), 0, s, acc, M, N, mult, shift, 64, (int64_t*)out);
+  else return hipErrorInvalidValue;
   return hipGetLastError();
 }
 
@@ -1434,10 +1529,56 @@ hipError_t rope(int16_t* qkv, int M, const int32_t* pos, const int32_t* cosT, co
 }
 
 hipError_t silu_gate(const int16_t* gu, int M, const int32_t* silu, int sh, int bits, uint8_t* planes, void* plain,
-                     hipStream_t s) {
+                     hipStream_t s, int32_t* sg_out) {
   dim3 grid(blocks_for((size_t)M * kDFF));
-  if (bits == 16) hipLaunchKernelGGL(silu_kernel<2>, grid, dim3(256), 0, s, gu, M, silu, sh, bits, planes, plain);
-  else hipLaunchKernelGGL(silu_kernel<4>, grid, dim3(256), 0, s, gu, M, silu, sh, bits, planes, plain);
+  if (bits == 16) hipLaunchKernelGGL(silu_kernel<2>, grid, dim3(256), 0, s, gu, M, silu, sh, bits, planes, plain, sg_out);
+  else hipLaunchKernelGGL(silu_kernel<4>, grid, dim3(256), 0, s, gu, M, silu, sh, bits, planes, plain, sg_out);
+  return hipGetLastError();
+}
+
+// Scores and probabilities of every (sequence, head, query) row for traces (python/intref.py:238-253,
+// its attn_score / attn_prob): one wave per row, lanes over the keys; the scores are written first and
+// read back by the same lanes.  score_out int16 [B][9][T][T] (0 past the diagonal), prob_out int32
+// [B][9][T][T]; sequence b holds rows b T .. b T + T - 1 of qkv.
+__global__ __launch_bounds__(64) void attn_trace_kernel(const int16_t* qkv, int T, const int32_t* exp_tab, int shift_s,
+                                                        int16_t* score_out, int32_t* prob_out) {
+  const int qi = blockIdx.x, hh = blockIdx.y, b = blockIdx.z, lane = threadIdx.x, g = hh / 3;
+  const int16_t* q = qkv + ((size_t)b * T + qi) * kQKVN + hh * 64;
+  const size_t orow = (((size_t)b * kNH + hh) * T + qi) * T;
+  int32_t mx = INT32_MIN;
+  for (int j = lane; j < T; j += 64) {
+    int32_t sv = 0;
+    if (j <= qi) {
+      const int16_t* k = qkv + ((size_t)b * T + j) * kQKVN + kD + g * 64;
+      int64_t acc = 0;
+      for (int d = 0; d < 64; ++d) acc += (int64_t)q[d] * k[d];
+      sv = (int32_t)sat(rs(acc, shift_s), 16);
+      mx = max(mx, sv);
+    }
+    score_out[orow + j] = (int16_t)sv;
+  }
+  for (int o = 32; o > 0; o >>= 1) mx = max(mx, __shfl_xor(mx, o));
+  int64_t Z = 0;
+  for (int j = lane; j <= qi; j += 64) {
+    const int d = mx - score_out[orow + j];
+    Z += d <= kDMax ? exp_tab[d] : 0;
+  }
+  for (int o = 32; o > 0; o >>= 1) Z += __shfl_xor(Z, o);
+  for (int j = lane; j < T; j += 64) {
+    int32_t P = 0;
+    if (j <= qi) {
+      const int d = mx - score_out[orow + j];
+      const int64_t e = d <= kDMax ? exp_tab[d] : 0;
+      P = (int32_t)((e * 65536 + Z / 2) / Z);
+    }
+    prob_out[orow + j] = P;
+  }
+}
+
+hipError_t attn_trace(const int16_t* qkv, int B, int T, const int32_t* exp_tab, int shift_s, int16_t* score_out,
+                      int32_t* prob_out, hipStream_t s) {
+  if (B <= 0 || T <= 0 || shift_s < 1) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(attn_trace_kernel, dim3(T, kNH, B), dim3(64), 0, s, qkv, T, exp_tab, shift_s, score_out, prob_out);
   return hipGetLastError();
 }
 

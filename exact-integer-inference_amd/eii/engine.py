@@ -129,7 +129,17 @@ class Engine:
             for s, w in width.items():
                 dt = torch.int16 if bits[s] == 16 else torch.int32
                 bufs[s] = torch.empty((B * T, w), dtype=dt, device=self.device)
-            bufs["resid_mid"] = torch.empty((B * T, D), dtype=torch.int32, device=self.device)
+            dev, M = self.device, B * T
+            bufs["resid_mid"] = torch.empty((M, D), dtype=torch.int32, device=dev)
+            # norm internals, attention matrices and the unsaturated residual updates (include/eii.h)
+            for n in ("norm1", "norm2"):
+                bufs[n + "_U"] = torch.empty(M, dtype=torch.int32, device=dev)
+                bufs[n + "_z"] = torch.empty((M, D), dtype=torch.int32, device=dev)
+            bufs["attn_score"] = torch.empty((B, 9, T, T), dtype=torch.int16, device=dev)
+            bufs["attn_prob"] = torch.empty((B, 9, T, T), dtype=torch.int32, device=dev)
+            bufs["o_res"] = torch.empty((M, D), dtype=torch.int64, device=dev)
+            bufs["down_res"] = torch.empty((M, D), dtype=torch.int64, device=dev)
+            bufs["silu_gate"] = torch.empty((M, 1536), dtype=torch.int32, device=dev)
             tr = L.eii_trace(**{k: v.data_ptr() for k, v in bufs.items()})
         L.check(self.lib.eii_block(self.h, layer, _ptr(x), B, T, C.byref(tr) if tr is not None else None, _stream()))
         return bufs

@@ -23,10 +23,14 @@ class EIIError(RuntimeError):
         self.code = code
 
 
+TRACE_SITES = ("norm1_out", "q_proj", "k_proj", "v_proj", "q_rope", "k_rope", "attn_ctx", "resid_mid",
+               "norm2_out", "gate_proj", "up_proj", "mlp_gated",
+               "norm1_U", "norm1_z", "attn_score", "attn_prob", "o_res", "norm2_U", "norm2_z", "silu_gate",
+               "down_res")
+
+
 class eii_trace(C.Structure):
-    _fields_ = [(n, vp) for n in ("norm1_out", "q_proj", "k_proj", "v_proj", "q_rope", "k_rope",
-                                  "attn_ctx", "resid_mid", "norm2_out", "gate_proj", "up_proj",
-                                  "mlp_gated")]
+    _fields_ = [(n, vp) for n in TRACE_SITES]
 
 
 # name -> (restype, argtypes); every entry point include/eii.h declares

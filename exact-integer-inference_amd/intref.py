@@ -14,9 +14,14 @@ implements).  Differences, all deliberate:
   * forward/embed/block/rmsnorm/linear/matmul_exact run on the GPU through libeii.so and
     raise when it is missing; there is no CPU path.  rs, sat, dequant and the quantizers are
     the reference's host-side elementwise helpers (its callers apply them to host arrays).
-  * block(..., trace) fills the trace keys the engine can dump (every activation site,
-    resid_in/resid_mid/resid_out); the reference's norm internals (_U, _z), attention
-    scores/probabilities and o_res/down_res/silu_gate are not produced.
+  * block(..., trace) fills every key the reference's does (python/intref.py:183,198-285):
+    resid_in/_mid/_out, _f, norm1/norm2 _U/_z/_out, the projections, q/k_rope, attn_score and
+    attn_prob [9, T, T], attn_ctx, o_res, silu_gate, mlp_gated, down_res -- all computed on the
+    GPU (the scores and probabilities by a trace-only kernel, o_res/down_res from the exact int64
+    accumulators).
+  * prop holds, for every format site the forward reads ("site|l", "final_out|30"), the class
+    and k the reference's scaling_proposal.json entry implies, rebuilt from model.bin's fm
+    records (flagged iff 32 bits; k = bits - 1 - f), as python/export_vectors.py:27,54 reads it.
   * forward_batch(ids [B, T]) is an addition: B independent sequences in one call.
 """
 import math
@@ -84,11 +89,21 @@ def _torch():
 
 
 def _width(bound):
+    if bound <= 1 << 7:
+        return 8
     if bound <= 1 << 15:
         return 16
     if bound <= 1 << 31:
         return 32
     raise ValueError(f"activation bound {bound} exceeds the engine's 32-bit limb inputs")
+
+
+_NP_OF_BITS = {8: np.int8, 16: np.int16, 32: np.int32}
+
+
+def _fits(a, bits):
+    a = np.asarray(a)
+    return a.size == 0 or (int(a.min()) >= -(1 << (bits - 1)) and int(a.max()) < (1 << (bits - 1)))
 
 
 def _dev(a, dtype):
@@ -97,18 +112,20 @@ def _dev(a, dtype):
 
 
 def matmul_exact(A, Wf, bound_a, wmax=127):      # python/intref.py:58-63
-    """Exact int64 A [T, K] @ W [N, K]^T on the int8 MFMA path (int8-valued W, |A| <= 2^31)."""
+    """Exact int64 A [T, K] @ W [N, K]^T on the int8 MFMA path (int8-valued W, |A| <= 2^31, any K)."""
     import ctypes as C
     from eii import lib as L
     A = np.asarray(A)
     K = A.shape[1]
     assert bound_a * wmax * K < 2.0 ** 53, "float64 accumulation would not be exact"
     W = np.asarray(Wf, dtype=np.float64)
-    if wmax > 127 or np.abs(W).max(initial=0) > 127 or np.any(W != np.rint(W)):
+    if W.min(initial=0) < -128 or W.max(initial=0) > 127 or np.any(W != np.rint(W)):
         raise ValueError("matmul_exact on the engine needs int8 weights")
     bits = _width(bound_a)
+    if not _fits(A, bits):
+        raise ValueError(f"A holds values outside the {bits}-bit range its bound {bound_a} implies")
     torch = _torch()
-    a = _dev(A, np.int16 if bits == 16 else np.int32)
+    a = _dev(A, _NP_OF_BITS[bits])
     w = _dev(W, np.int8)
     N = W.shape[0]
     pad = (-N) % 4                                   # the kernels take N in multiples of 4
@@ -140,6 +157,19 @@ class Model:
                        for L in self.bin.layers]
         self.rope = (self.bin.rope_cos, self.bin.rope_sin)
         self.f_y = self.bin.f_y
+        self.prop = self._prop()
+
+    def _prop(self):
+        """python/intref.py:138 `prop` for the sites the forward reads, rebuilt from the fm records:
+        Model.fmt's rule (flagged -> (32, 31 - k), else (16, 15 - k)) inverted."""
+        prop = {}
+        for l in range(self.L):
+            for site in _mb.SITES:
+                bits, f = self.bin.fmt(site, l)
+                prop[f"{site}|{l}"] = {"class": "flagged_wide_int32" if bits == 32 else "int16_per_tensor",
+                                       "k": bits - 1 - f, "f": f}
+        prop[f"final_out|{self.L}"] = {"class": "int16_per_tensor", "k": 15 - self.f_y, "f": self.f_y}
+        return prop
 
     def fmt(self, site, l):                          # python/intref.py:154-160
         if site == "final_out" and l == self.L:
@@ -156,6 +186,8 @@ class Model:
         x = np.asarray(x)
         assert x.shape[1] == _mb.D and x.min(initial=0) >= -2 ** 31 and x.max(initial=0) < 2 ** 31
         wq, fw = gain
+        if not _fits(wq, 32):
+            raise ValueError("rmsnorm on the engine takes gains inside int32")
         xd, gd = _dev(x, np.int32), _dev(wq, np.int32)
         out = torch.empty(x.shape, dtype=torch.int16 if bits_out == 16 else torch.int32, device=xd.device)
         L.check(L.load().eii_rmsnorm(C.c_void_p(xd.data_ptr()), x.shape[0], C.c_void_p(gd.data_ptr()), fw, f_out,
@@ -172,15 +204,17 @@ class Model:
         torch = _torch()
         q, m, n = W
         acc = matmul_exact(a, q, bound_a)
-        assert np.abs(acc).max(initial=0) * int(np.max(m)) < 2 ** 63
+        assert np.abs(acc).max() * int(m.max()) < 2 ** 63
         bits = _width(bound_a)
-        a_d = _dev(a, np.int16 if bits == 16 else np.int32)
+        a_d = _dev(a, _NP_OF_BITS[bits])
         w_d = _dev(q, np.int8)
         N, K = w_d.shape
         if N % 4:
             raise ValueError("linear on the engine needs N a multiple of 4")
         shift = np.asarray(n, dtype=I64) + f_in - f_out
         assert (shift >= 1).all(), "per-element shift must be >= 1"
+        if not _fits(m, 32) or not _fits(shift, 32):
+            raise ValueError("linear on the engine takes multipliers and shifts inside int32")
         ws = torch.empty(N, dtype=torch.int32, device=w_d.device)
         st = C.c_void_p(torch.cuda.current_stream().cuda_stream)
         lib = L.load()
@@ -203,8 +237,14 @@ class Model:
         out = xd.cpu().numpy().astype(I64)
         if trace is not None:
             for k, v in bufs.items():
-                trace[k] = v.cpu().numpy().astype(I64)
+                v = v.cpu().numpy().astype(I64)
+                trace[k] = v[0] if k in ("attn_score", "attn_prob") else v   # [9, T, T] for the one sequence
             trace["resid_out"] = out.copy()
+            f = {s: self.fmt(s, l)[1] for s in _mb.SITES}
+            bits_m, f_m0 = self.fmt("mlp_gated", l)
+            f["mlp_gated"] = min(f_m0, f["silu_gate"] + f["up_proj"]) if bits_m == 32 else f_m0
+            trace["_f"] = {"resid_in": F_RES, "o_res": F_RES, "resid_mid": F_RES, "down_res": F_RES,
+                           "resid_out": F_RES, "attn_score": F_SCORE, "attn_prob": 16, **f}
         return out
 
     def forward(self, ids, narrow_residual=False):   # python/intref.py:288-301

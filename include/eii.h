@@ -27,13 +27,20 @@ extern "C" {
 
 typedef struct eii_model eii_model;
 
-/* Optional per-site dumps of one block (python/intref.py:198-285 `trace`).  Each non-NULL
+/* Optional per-site dumps of one block (python/intref.py:183,198-285 `trace`).  Each non-NULL
  * pointer receives [rows, width] values in the site's declared width: int16 for 16-bit sites,
- * int32 for 32-bit sites (widths: q/norm/ctx 576, k/v 192, gate/up/gated 1536). */
+ * int32 for 32-bit sites (widths: q/norm/ctx 576, k/v 192, gate/up/gated 1536).  The norm
+ * internals, attention matrices and unsaturated residual updates have fixed types:
+ *   norm1_U, norm2_U int32 [rows]; norm1_z, norm2_z int32 [rows, 576] (|z| <= 2^24);
+ *   attn_score int16 [B, 9, T, T] (0 past the diagonal), attn_prob int32 [B, 9, T, T] (Q0.16);
+ *   o_res, down_res int64 [rows, 576] (RS(acc m, .) before the saturating add);
+ *   silu_gate int32 [rows, 1536] (the SiLU table values). */
 typedef struct {
   void* norm1_out; void* q_proj; void* k_proj; void* v_proj; void* q_rope; void* k_rope;
   void* attn_ctx; int32_t* resid_mid; void* norm2_out; void* gate_proj; void* up_proj;
   void* mlp_gated;
+  int32_t* norm1_U; int32_t* norm1_z; int16_t* attn_score; int32_t* attn_prob; int64_t* o_res;
+  int32_t* norm2_U; int32_t* norm2_z; int32_t* silu_gate; int64_t* down_res;
 } eii_trace;
 
 const char* eii_last_error(void);
@@ -131,9 +138,9 @@ int eii_argmax(const int32_t* logits_dev, int rows, int n, int64_t* out_dev, voi
 /* Row sums of int8 weights W_dev [N, K] into wsum_dev int32 [N]. */
 int eii_weight_colsum(const int8_t* W_dev, int N, int K, int32_t* wsum_dev, void* stream);
 
-/* Exact acc_dev int64 [M, N] = A W^T (python/intref.py:58-63 matmul_exact) with A_dev int16
- * (a_bits 16) or int32 (a_bits 32) [M, K], W_dev int8 [N, K]; K in {64, 128, 576, 1536},
- * N a multiple of 4. */
+/* Exact acc_dev int64 [M, N] = A W^T (python/intref.py:58-63 matmul_exact) with A_dev int8
+ * (a_bits 8), int16 (16) or int32 (32) [M, K], W_dev int8 [N, K]; any K up to 131072 (zero-padded
+ * to a multiple of 64 inside, which adds nothing), N a multiple of 4, M * K <= 2^31. */
 int eii_gemm_i8(const void* A_dev, int a_bits, const int8_t* W_dev, int M, int N, int K,
                 int64_t* acc_dev, void* stream);
 /* The same with precomputed row sums (eii_weight_colsum). */
@@ -141,15 +148,19 @@ int eii_gemm_i8_ws(const void* A_dev, int a_bits, const int8_t* W_dev, const int
                    int M, int N, int K, int64_t* acc_dev, void* stream);
 
 /* Linear with requantization (python/intref.py:186-190):
- * out = SAT(RS(acc * mult[n], shift[n]), out_bits), shift[n] = n + f_in - f_out >= 1;
- * out_dev int16 (out_bits 16) or int32 (out_bits 32) [M, N]. */
+ * out = SAT(RS(acc * mult[n], shift[n]), out_bits) evaluated in int64 on the exact accumulators,
+ * for any int32 mult and shift[n] = n + f_in - f_out (the reference asserts shift >= 1 and
+ * max |acc| * max mult < 2^63; a shift <= 0 is a left shift as RS defines it);
+ * out_dev int16 (out_bits 16) or int32 (out_bits 32) [M, N].  A, W, M, N, K as eii_gemm_i8. */
 int eii_linear(const void* A_dev, int a_bits, const int8_t* W_dev, const int32_t* wsum_dev,
                const int32_t* mult_dev, const int32_t* shift_dev, int M, int N, int K,
                int out_bits, void* out_dev, void* stream);
 
 /* RMSNorm (python/intref.py:168-184): x_dev int32 [M, 576] -> out_dev [M, 576] of out_bits
- * (16 -> int16, 32 -> int32); gain_dev int32 [576] with exponent f_gain; the three pointers
- * 16-byte aligned. */
+ * (16 -> int16, 32 -> int32); gain_dev int32 [576] with exponent f_gain, any int32 gain (3 z gain
+ * formed in int64 and saturated before narrowing, as c/intref.c:106-108); the three pointers
+ * 16-byte aligned.  (A model.bin's gains must be int16, as quant_vec_int16 makes them,
+ * python/intref.py:126-130; eii_model_load rejects wider ones with status 4.) */
 int eii_rmsnorm(const int32_t* x_dev, int M, const int32_t* gain_dev, int f_gain, int f_out,
                 int out_bits, void* out_dev, void* stream);
 

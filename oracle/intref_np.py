@@ -139,7 +139,7 @@ class OracleModel:
         acc = z * wq[None, :] * 3
         out = sat(rs(acc, 21 + fw - f_out), bits_out)
         if trace is not None:
-            trace[tag + "_U"] = U; trace[tag + "_out"] = out
+            trace[tag + "_U"] = U; trace[tag + "_z"] = z; trace[tag + "_out"] = out
         return out
 
     def linear(self, a, bound_a, W, f_in, f_out, bits_out, key=None):   # python/intref.py:186-190
@@ -195,6 +195,8 @@ class OracleModel:
         pos = np.tile(np.arange(T), B)
         if tr is not None:
             tr["resid_in"] = x.copy()
+            tr["_f"] = {"resid_in": F_RES, "o_res": F_RES, "resid_mid": F_RES, "down_res": F_RES,
+                        "resid_out": F_RES, "attn_score": F_SCORE, "attn_prob": 16}   # python/intref.py:199-201
 
         bits_h, f_h = self.fmt("norm1_out", l)
         h = self.rmsnorm(x, Ly["ln1"], f_h, bits_h, tr, "norm1")
@@ -216,6 +218,8 @@ class OracleModel:
         bits_c, f_c = self.fmt("attn_ctx", l)
         vv = v.reshape(R, NKV, HD)
         ctx = np.empty((R, NH, HD), dtype=I64)
+        if tr is not None and B == 1:
+            tr["attn_score"], tr["attn_prob"] = [], []
         for b in range(B):
             sl = slice(b * T, (b + 1) * T)
             ctx[sl] = self.attention(qr[sl], kr[sl], vv[sl], shift_s, f_v, f_c, bits_c,
@@ -223,6 +227,8 @@ class OracleModel:
         ctx = ctx.reshape(R, D)
         if tr is not None:
             tr["attn_ctx"] = ctx
+            if B == 1:                                            # python/intref.py:252-253
+                tr["attn_score"] = np.stack(tr["attn_score"]); tr["attn_prob"] = np.stack(tr["attn_prob"])
 
         q_o, m_o, n_o = Ly["o"]                                   # python/intref.py:257-261
         acc = matmul_exact(ctx, self.wf((l, "o"), q_o), 1 << (bits_c - 1))
@@ -251,6 +257,9 @@ class OracleModel:
         if tr is not None:
             tr.update(norm2_out=h2, gate_proj=g_, up_proj=u_, silu_gate=sg, mlp_gated=gated,
                       down_res=d_res, resid_out=x.copy())
+            tr["_f"].update(norm1_out=f_h, q_proj=f_q, k_proj=f_k, v_proj=f_v, q_rope=f_qr, k_rope=f_kr,
+                            attn_ctx=f_c, norm2_out=f_h2, gate_proj=f_g, up_proj=f_u, silu_gate=f_s,
+                            mlp_gated=f_m)                    # python/intref.py:284-285
         return x
 
     def final(self, x):                               # python/intref.py:296-301

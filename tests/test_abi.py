@@ -39,9 +39,10 @@ def test_argument_errors_need_no_device():
     assert lib.eii_gemm_i8(None, 16, None, 4, 4, 64, None, None) == L.EII_E_ARG
     a = (C.c_int16 * 64)()
     w = (C.c_int8 * 256)()
-    assert lib.eii_gemm_i8(a, 8, w, 1, 4, 64, None, None) == L.EII_E_ARG        # a_bits
-    assert lib.eii_gemm_i8(a, 16, w, 1, 4, 100, None, None) == L.EII_E_ARG      # K
-    assert b"K must be" in lib.eii_last_error()
+    assert lib.eii_gemm_i8(a, 12, w, 1, 4, 64, a, None) == L.EII_E_ARG         # a_bits
+    assert lib.eii_gemm_i8(a, 8, w, 1, 4, 64, None, None) == L.EII_E_ARG        # no output
+    assert lib.eii_gemm_i8(a, 16, w, 1, 4, 200000, a, None) == L.EII_E_BOUND    # K past 131072
+    assert b"131072" in lib.eii_last_error()
     assert lib.eii_linear(a, 16, w, None, None, None, 1, 4, 64, 16, None, None) == L.EII_E_ARG
     assert lib.eii_rmsnorm(None, 1, None, 14, 11, 16, None, None) == L.EII_E_ARG
     assert lib.eii_attention(None, None, 1, 4, None, 10, 10, 11, 11, 16, None, None) == L.EII_E_ARG
@@ -77,3 +78,28 @@ def test_model_file_errors(tmp_path, model_path):
         f.write(np.array([-40], dtype="<i8").tobytes())
     assert lib.eii_model_load(str(bad).encode(), 0, C.byref(h)) == L.EII_E_BOUND
     assert not h.value
+
+
+def test_model_gain_outside_int16(tmp_path, model_path):
+    """RMSNorm gains are int16 (quant_vec_int16, python/intref.py:126-130): a wider one is a bound
+    violation at load, before any device work."""
+    lib = L.load()
+    h = C.c_void_p()
+    for layer, which in ((0, 0), (17, 1)):
+        bad = tmp_path / f"gain{layer}.bin"
+        shutil.copyfile(model_path, bad)
+        off = modelbin.HEADER_BYTES + layer * modelbin.LAYER_BYTES + 24 * 8 + which * (576 * 8 + 8) + 8 * 5
+        with open(bad, "r+b") as f:
+            f.seek(off)
+            f.write(np.array([1 << 20], dtype="<i8").tobytes())
+        assert lib.eii_model_load(str(bad).encode(), 0, C.byref(h)) == L.EII_E_BOUND
+        assert b"ln%d" % (which + 1) in lib.eii_last_error()
+        assert not h.value
+    bad = tmp_path / "final.bin"
+    shutil.copyfile(model_path, bad)
+    off = 49152 * 576 + 2 * 49152 * 8 + 8 * 100        # final gain entry 100
+    with open(bad, "r+b") as f:
+        f.seek(off)
+        f.write(np.array([-32769], dtype="<i8").tobytes())
+    assert lib.eii_model_load(str(bad).encode(), 0, C.byref(h)) == L.EII_E_BOUND
+    assert b"final gain" in lib.eii_last_error()

@@ -1053,6 +1053,56 @@ extern "C" int eii_gemm_i8(const void* A, int a_bits, const int8_t* W, int M, in
   return gemm_i8_staged(A, a_bits, W, ws, M, N, K, acc, st, s);
 }
 
+// ---- allocation-free exact matmul
+// Staging for eii_gemm_i8_ws_noalloc: a file-scope device array, one copy per GPU the library runs
+// on, held until the process ends.  In host code `scratch` names a host-side stand-in, not device
+// memory: its device address on the current GPU comes from hipGetSymbolAddress, once per device, and
+// only that address is handed to kernels.
+constexpr size_t kScratchBytes = (size_t)64 << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+static std::mutex g_scratch_mu;
+static uint8_t* g_scratch_dev[kMaxDevices];
+
+static int scratch_on_current_device(uint8_t** out) {
+  int dev = 0;
+  HIPCHK(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices) return fail(EII_E_DEVICE, "device ordinal out of range");
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(EII_E_DEVICE, std::string("scratch address: ") + hipGetErrorString(e));
+    g_scratch_dev[dev] = (uint8_t*)p;
+  }
+  *out = g_scratch_dev[dev];
+  return EII_OK;
+}
+
+extern "C" int eii_gemm_i8_ws_noalloc(const void* A, int a_bits, const int8_t* W, const int32_t* wsum, int M, int N,
+                                      int K, int64_t* acc, void* stream) {
+  int rc;
+  if ((rc = check_gemm_args(A, a_bits, W, M, N, K))) return rc;
+  if (!wsum || !acc) return fail(EII_E_ARG, "null output");
+  if (N % 4) return fail(EII_E_ARG, "N must be a multiple of 4");
+  const int Kp = padded_k(K);
+  const size_t plane_bytes = Staging::align((size_t)M * Kp * limb_planes(a_bits));
+  if (plane_bytes + swizzled_bytes(N, Kp) > kScratchBytes)
+    return fail(EII_E_BOUND, "operands need " + std::to_string(plane_bytes + swizzled_bytes(N, Kp)) +
+                                 " bytes of staging, above the 64 MiB scratch of the allocation-free entry point");
+  uint8_t* base = nullptr;
+  if ((rc = scratch_on_current_device(&base))) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  // every byte the GEMM reads is written here first (planes over all of K padded, weights over every
+  // 32-row block): nothing in the scratch needs clearing
+  uint8_t* planes = base;
+  int8_t* wf = (int8_t*)(base + plane_bytes);
+  if ((rc = stage_operands_at(A, a_bits, W, M, N, K, planes, wf, s))) return rc;
+  const hipError_t e = gemm_i64_anyk(planes, limb_planes(a_bits), wf, wsum, M, N, Kp, acc, s);
+  if (e != hipSuccess) return fail(EII_E_DEVICE, std::string("eii_gemm_i8_ws_noalloc: ") + hipGetErrorString(e));
+  return EII_OK;
+}
+
 // The requantization runs on the exact int64 accumulators, in int64 as python/intref.py:189 does,
 // so any int32 multiplier and shift behave as there (the reference asserts |acc| max m < 2^63).
 extern "C" int eii_linear(const void* A, int a_bits, const int8_t* W, const int32_t* wsum, const int32_t* mult,

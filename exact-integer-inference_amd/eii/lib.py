@@ -58,6 +58,7 @@ SIGNATURES = {
     "eii_weight_colsum": (i32, [vp, i32, i32, vp, vp]),
     "eii_gemm_i8": (i32, [vp, i32, vp, i32, i32, i32, vp, vp]),
     "eii_gemm_i8_ws": (i32, [vp, i32, vp, vp, i32, i32, i32, vp, vp]),
+    "eii_gemm_i8_ws_noalloc": (i32, [vp, i32, vp, vp, i32, i32, i32, vp, vp]),
     "eii_linear": (i32, [vp, i32, vp, vp, vp, vp, i32, i32, i32, i32, vp, vp]),
     "eii_rmsnorm": (i32, [vp, i32, vp, i32, i32, i32, vp, vp]),
     "eii_attention": (i32, [vp, vp, i32, i32, vp, i32, i32, i32, i32, i32, vp, vp]),

@@ -147,6 +147,16 @@ int eii_gemm_i8(const void* A_dev, int a_bits, const int8_t* W_dev, int M, int N
 int eii_gemm_i8_ws(const void* A_dev, int a_bits, const int8_t* W_dev, const int32_t* wsum_dev,
                    int M, int N, int K, int64_t* acc_dev, void* stream);
 
+/* eii_gemm_i8_ws without any allocation: no counterpart in the reference.  For callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Operands are staged in a fixed 64 MiB device array per GPU that the library holds
+ * until the process ends; needing more than that (limb planes of M x K rounded up to 64 columns,
+ * 2 planes for 8/16-bit A and 4 for 32-bit, plus N rounded up to 32 rows x K weight bytes) is
+ * status 4.  Calls on one GPU share that array: calls whose work overlaps on one GPU (different
+ * streams, or host threads without ordering) race and must be serialized by the caller. */
+int eii_gemm_i8_ws_noalloc(const void* A_dev, int a_bits, const int8_t* W_dev, const int32_t* wsum_dev,
+                           int M, int N, int K, int64_t* acc_dev, void* stream);
+
 /* Linear with requantization (python/intref.py:186-190):
  * out = SAT(RS(acc * mult[n], shift[n]), out_bits) evaluated in int64 on the exact accumulators,
  * for any int32 mult and shift[n] = n + f_in - f_out (the reference asserts shift >= 1 and

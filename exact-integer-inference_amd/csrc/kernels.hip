@@ -69,6 +69,7 @@ __device__ __forceinline__ uint32_t limb_word(const int32_t* v, int l, int W) {
 // offset turns the reference's round-half-up into a tie-free rounding).  4-limb inputs, whose
 // acc * m reaches 2^62, use int64.
 constexpr double kMagic = 6755399441055744.0;   // 1.5 * 2^52: y + kMagic rounds y to an integer
+constexpr int kLoopPrio = 3;                     // wave priority of the GEMM main loop (epilogues run at 0)
 
 __device__ __forceinline__ int32_t rne_i32(double y) {   // |y| < 2^31 after clamping
   return (int32_t)(uint32_t)(uint64_t)__double_as_longlong(y + kMagic);
@@ -90,18 +91,26 @@ __device__ __forceinline__ v16i mfma32(v4i a, v4i b, v16i c) {
 // D[m][n] = sum_k a[m,k] W[n,k].  Lane = 32 h + c, register j = 4 b + r holds row
 // i = 8 b + 4 h + r, column c of the 32x32 tile: the 32 lanes of a half-wave hold 32
 // consecutive columns of one row, so every epilogue store is a contiguous run.
-// NARROW: 64 x 192 tiles for N a multiple of 192 but not of 128 (N = 576: three column blocks
-// instead of four and a half, so the persistent workgroups get evenly sized tiles and no
-// half-empty ones), 2-limb activations only.
-template <int AW, bool NARROW = false>
+// Tile shapes (4 waves, each 32 TM rows x 32 TN columns):
+//   kShapeSquare: 2 x 2 waves, 128 x 128 tiles for 2-limb activations, 64 x 128 for 4-limb;
+//   kShapeNarrow: 2 x 2 waves, 64 x 192 tiles for N a multiple of 192 but not of 128 (N = 576: three
+//     column blocks instead of four and a half, so the persistent workgroups get evenly sized tiles and
+//     no half-empty ones), 2-limb activations only;
+//   kShapeRow: 1 x 4 waves, 64 x 256 tiles for wide 2-limb GEMMs (q/k/v, gate/up, the head): the four
+//     waves share one 64-row activation tile in LDS (half the LDS traffic of a 128-row tile per MFMA
+//     column) and each loads its own weight columns.
+constexpr int kShapeSquare = 0, kShapeNarrow = 1, kShapeRow = 2;
+template <int AW, int SHAPE = kShapeSquare>
 struct GemmCfg {
-  static_assert(!NARROW || AW == 2, "narrow tiles for 2-limb activations");
+  static_assert(SHAPE == kShapeSquare || AW == 2, "narrow and row tiles for 2-limb activations");
   static constexpr int kThreads = 256;                   // 4 waves; two workgroups share a CU
-  static constexpr int BM = AW == 2 && !NARROW ? 128 : 64, BN = NARROW ? 192 : 128;
-  static constexpr int WM = BM / 2, WN = BN / 2;         // 2 x 2 waves
+  static constexpr int WGM = SHAPE == kShapeRow ? 1 : 2, WGN = 4 / WGM;   // wave grid
+  static constexpr int BM = SHAPE == kShapeSquare && AW == 2 ? 128 : 64;
+  static constexpr int BN = SHAPE == kShapeNarrow ? 192 : SHAPE == kShapeRow ? 256 : 128;
+  static constexpr int WM = BM / WGM, WN = BN / WGN;     // wave tile
   static constexpr int TM = WM / 32, TN = WN / 32;       // 32x32 tiles per wave
   static constexpr int kPlane = BM * kLdsRow;
-  static constexpr int kStage = AW * kPlane;              // activation limb planes only: 16 KB
+  static constexpr int kStage = AW * kPlane;              // activation limb planes only: 8 or 16 KB
   static constexpr int kStages = 4;                       // loaded two and three steps ahead
   static constexpr int kAChunks = AW * BM * 4 / kThreads;   // 16-byte direct-to-LDS loads per thread
   static_assert(kAChunks * kThreads == AW * BM * 4, "chunk split");
@@ -120,11 +129,13 @@ __device__ __forceinline__ void tile_coords(int v, int nMB, int nNB, int& mb, in
 
 __device__ __forceinline__ uint32_t pack16(int32_t a, int32_t b) { return (uint32_t)(a & 0xFFFF) | ((uint32_t)b << 16); }
 
-template <int AW, int EPI, int NK, bool NARROW>
+template <int AW, int EPI, int NK, int SHAPE>
 __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
-  using C = GemmCfg<AW, NARROW>;
-  static_assert(!NARROW || EPI == EPI_RESID || EPI == EPI_I64 || EPI == EPI_REQ16 || EPI == EPI_REQ32 ||
-                EPI == EPI_LOGITS, "the SiLU and QKV epilogues pair columns 32 apart within 64-column blocks");
+  using C = GemmCfg<AW, SHAPE>;
+  static_assert(SHAPE != kShapeNarrow || EPI == EPI_RESID || EPI == EPI_I64 || EPI == EPI_REQ16 ||
+                EPI == EPI_REQ32 || EPI == EPI_LOGITS,
+                "the SiLU and QKV epilogues pair columns 32 apart within 64-column blocks");
+  static_assert((EPI != EPI_SILU && EPI != EPI_QKV) || C::WN == 64, "one 64-column pair block per wave");
   static_assert(NK >= 1, "at least one K block");
   // EPI_SILU: entries 32768 - kTabHalf .. 32768 + kTabHalf - 1 of a 16-bit SiLU table as int16
   // after the stages (the gate values cluster around 0, so most table reads hit LDS)
@@ -148,7 +159,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
   }
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / C::WGN, wn = wave % C::WGN;
   const int fc = lane & 31, fh = lane >> 5;
   const uint8_t* Ab = (const uint8_t*)g.A;
 
@@ -390,8 +401,9 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
         // RS(x, sh) = RNE(x 2^-sh + 2^-(sh+1)) for sh >= 1; for sh <= 0 the scaled value is an integer
         const double sc = ldexp(1.0, -g.sh2), half = g.sh2 >= 1 ? ldexp(0.5, -g.sh2) : 0.0;
         const size_t pl = (size_t)g.M * (N / 2);
-        uint8_t* tb = (uint8_t*)g.out + (size_t)nb * g.M * 64 + (size_t)m0 * 64;
-        const uint32_t lane_b4 = (uint32_t)(rw + (fc & 3)) * 64u + (uint32_t)(wn * 32 + (fc & ~3));
+        // gated columns nb BN / 2 + 32 wn .. + 31: K block (nb BN / 2 + 32 wn) / 64, offset 32 (wn % 2)
+        uint8_t* tb = (uint8_t*)g.out + (size_t)(nb * (C::BN / 128) + (wn >> 1)) * g.M * 64 + (size_t)m0 * 64;
+        const uint32_t lane_b4 = (uint32_t)(rw + (fc & 3)) * 64u + (uint32_t)((wn & 1) * 32 + (fc & ~3));
 #pragma unroll
         for (int tm = 0; tm < C::TM; ++tm) {
           int32_t gv[16], sv[16];
@@ -537,6 +549,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
   // code up to its epilogue.
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
+  __builtin_amdgcn_s_setprio(kLoopPrio);
   a_step(0, 0, 0);
   a_step(1 / nk, 1 % nk, 1);
   w_step(I0{}, 0, 0);
@@ -583,9 +596,14 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
     if (kb != nk - 1) return;
 
     // ---------------------------------------------------------------- epilogue
+    // The epilogue runs at the lowest wave priority and the main loop at a raised one: the two
+    // workgroups of a CU share its SIMDs, so one workgroup's epilogue (vector work, stores) issues
+    // in the gaps of the other's MFMA loop instead of competing with it for issue slots.
     int mb, nb;
     coords(jt, mb, nb);
+    __builtin_amdgcn_s_setprio(0);
     epilogue(mb, nb);
+    __builtin_amdgcn_s_setprio(kLoopPrio);
 #pragma unroll
     for (int a = 0; a < C::TM; ++a)
 #pragma unroll
@@ -627,9 +645,9 @@ int device_cus() {
   return cus;
 }
 
-template <int AW, int EPI, bool NARROW>
+template <int AW, int EPI, int SHAPE>
 hipError_t launch_gemm_cfg(const GemmArgs& a, hipStream_t s) {
-  using C = GemmCfg<AW, NARROW>;
+  using C = GemmCfg<AW, SHAPE>;
   const int nT = ((a.M + C::BM - 1) / C::BM) * ((a.N + C::BN - 1) / C::BN);
   // two persistent workgroups per CU, a multiple of 8 so every XCD gets the same count
   const int per_xcd = std::min((nT + 7) / 8, std::max(1, 2 * device_cus() / 8));
@@ -638,22 +656,27 @@ hipError_t launch_gemm_cfg(const GemmArgs& a, hipStream_t s) {
   // (576, 1536) for every epilogue, and 64, 128 for the operator entry points
   constexpr bool op = EPI == EPI_I64 || EPI == EPI_REQ16 || EPI == EPI_REQ32;
   switch (a.K / kBK) {
-    case 9: hipLaunchKernelGGL((gemm_kernel<AW, EPI, 9, NARROW>), grid, block, 0, s, a); break;
-    case 24: hipLaunchKernelGGL((gemm_kernel<AW, EPI, 24, NARROW>), grid, block, 0, s, a); break;
-    case 1: if constexpr (op) { hipLaunchKernelGGL((gemm_kernel<AW, EPI, 1, NARROW>), grid, block, 0, s, a); break; }
+    case 9: hipLaunchKernelGGL((gemm_kernel<AW, EPI, 9, SHAPE>), grid, block, 0, s, a); break;
+    case 24: hipLaunchKernelGGL((gemm_kernel<AW, EPI, 24, SHAPE>), grid, block, 0, s, a); break;
+    case 1: if constexpr (op) { hipLaunchKernelGGL((gemm_kernel<AW, EPI, 1, SHAPE>), grid, block, 0, s, a); break; }
             return hipErrorInvalidValue;
-    case 2: if constexpr (op) { hipLaunchKernelGGL((gemm_kernel<AW, EPI, 2, NARROW>), grid, block, 0, s, a); break; }
+    case 2: if constexpr (op) { hipLaunchKernelGGL((gemm_kernel<AW, EPI, 2, SHAPE>), grid, block, 0, s, a); break; }
             return hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
 
+// Tile shape per launch: 64 x 192 for 2-limb residual GEMMs with N = 576, 64 x 256 for the wide
+// 2-limb GEMMs (q/k/v, gate/up, the head: N >= 768, at most 1/16 of a tile column idle at N = 960),
+// 128 x 128 (64 x 128 for 4 limbs) otherwise.
 template <int AW, int EPI>
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
   if constexpr (AW == 2 && EPI == EPI_RESID)
-    if (a.N % 192 == 0 && a.N % 128 != 0) return launch_gemm_cfg<AW, EPI, true>(a, s);
-  return launch_gemm_cfg<AW, EPI, false>(a, s);
+    if (a.N % 192 == 0 && a.N % 128 != 0) return launch_gemm_cfg<AW, EPI, kShapeNarrow>(a, s);
+  if constexpr (AW == 2 && EPI != EPI_RESID)
+    if (a.N >= 768) return launch_gemm_cfg<AW, EPI, kShapeRow>(a, s);
+  return launch_gemm_cfg<AW, EPI, kShapeSquare>(a, s);
 }
 
 // thread = 4 consecutive elements (k = 4 i .. 4 i + 3) of one row of the padded [M, Kp] operand

@@ -53,3 +53,35 @@ def test_extreme_int16_gains(extreme_model):
         assert np.array_equal(lg, ora.final(xo))
     finally:
         eng.close()
+
+
+@pytest.fixture(scope="module")
+def left_shift_model(tmp_path_factory, model_path):
+    """Layer 0's ln1 exponent lowered so the norm's output shift is -25: a left shift by 25 of values up
+    to 2^41, which wraps in the reference's int64 (the kernel's int64 path below shift -21)."""
+    p = tmp_path_factory.mktemp("lshift") / "model_norm_lshift.bin"
+    shutil.copyfile(model_path, p)
+    f_norm1 = int(modelbin.read(model_path).layers[0]["fm"][1])
+    with open(p, "r+b") as f:
+        f.seek(modelbin.HEADER_BYTES + 24 * 8 + 576 * 8)
+        f.write(np.array([-25 - 21 + f_norm1], dtype="<i8").tobytes())
+    return str(p)
+
+
+def test_norm_left_shift_wraps_like_int64(left_shift_model):
+    from eii.engine import Engine
+    from oracle.intref_np import OracleModel
+    ora = OracleModel(left_shift_model)
+    eng = Engine(left_shift_model)
+    try:
+        ids = synth.token_ids("cfg1")[0]
+        x0 = ora.embed(ids)
+        x = torch.from_numpy(x0.astype(np.int32)).cuda()
+        tr = eng.block(0, x, 1, len(ids), trace=True)
+        want = {}
+        ora.block(0, x0, len(ids), want)
+        for k in ("norm1_out", "norm1_U", "norm1_z"):
+            got = tr[k].cpu().numpy().astype(np.int64).reshape(want[k].shape)
+            assert np.array_equal(got, want[k]), k
+    finally:
+        eng.close()

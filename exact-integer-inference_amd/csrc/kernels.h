@@ -18,6 +18,9 @@ enum Epi : int {
   // W = q | k | v rows (N = 960, 16-bit outputs): RoPE on q heads (shift sh_q) and k heads (sh_k)
   // at positions pos[m] with cosT/sinT [rows, 32], out int16 [M, 960]        (python/intref.py:207-222)
   EPI_QKV = 6,
+  // EPI_SILU with a 16-bit table and a gated shift in 1..30 (|silu up| < 2^30): the gated product
+  // and its requantization in int32; gemm() selects it from EPI_SILU by itself
+  EPI_SILU_I = 7,
 };
 
 // Activations enter the GEMM as int8 limb planes (eii_int.h split_limbs): a_bytes planes of

@@ -135,11 +135,14 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
   static_assert(SHAPE != kShapeNarrow || EPI == EPI_RESID || EPI == EPI_I64 || EPI == EPI_REQ16 ||
                 EPI == EPI_REQ32 || EPI == EPI_LOGITS,
                 "the SiLU and QKV epilogues pair columns 32 apart within 64-column blocks");
-  static_assert((EPI != EPI_SILU && EPI != EPI_QKV) || C::WN == 64, "one 64-column pair block per wave");
+  constexpr bool kSilu = EPI == EPI_SILU || EPI == EPI_SILU_I;
+  static_assert((!kSilu && EPI != EPI_QKV) || C::WN == 64, "one 64-column pair block per wave");
   static_assert(NK >= 1, "at least one K block");
   // EPI_SILU: entries 32768 - kTabHalf .. 32768 + kTabHalf - 1 of a 16-bit SiLU table as int16
-  // after the stages (the gate values cluster around 0, so most table reads hit LDS)
-  constexpr int kTabHalf = 4096, kTabBytes = EPI == EPI_SILU ? 4 * kTabHalf : 0;
+  // after the stages (the gate values cluster around 0: with 64 x 256 tiles the window fills the CU's
+  // LDS beside two workgroups' stages, and about 0.3 % of the gates lie outside it)
+  constexpr int kTabHalf = 4096;
+  constexpr int kTabBytes = kSilu ? 4 * kTabHalf : 0;
   __shared__ __attribute__((aligned(16))) uint8_t smem[C::kStages * C::kStage + kTabBytes];
   const int nMB = (g.M + C::BM - 1) / C::BM, nNB = (g.N + C::BN - 1) / C::BN, nT = nMB * nNB;
   // this workgroup's tiles: v = v0, v0 + stride, ... < vend
@@ -150,7 +153,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
   constexpr int nk = NK;
   int16_t* const tabw = (int16_t*)(smem + C::kStages * C::kStage);
   int tab_half = 0;   // 0: no LDS window (32-bit table), every read goes to global memory
-  if constexpr (EPI == EPI_SILU) {
+  if constexpr (kSilu) {
     if (g.tab_bits == 16) {
       tab_half = kTabHalf;
       for (int i = threadIdx.x; i < 2 * kTabHalf; i += C::kThreads) tabw[i] = (int16_t)g.aux_tab[32768 - kTabHalf + i];
@@ -394,59 +397,66 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
         if constexpr (AW == 2) return rint(fmin(fmax(scaled(tm, tn, e), -32768.0), 32767.0));
         else return (double)value16(tm, tn, e);
       };
-      if constexpr (EPI == EPI_SILU) {
+      if constexpr (kSilu) {
         // gated limb planes (bits2 / 8 planes of M x N / 2, K-blocked): the lane's gated column
         // n0 / 2 + wn 32 + fc lies in 64-column block nb at offset wn 32 + fc
         const double lo = -ldexp(1.0, g.bits2 - 1), hi = ldexp(1.0, g.bits2 - 1) - 1.0;
         // RS(x, sh) = RNE(x 2^-sh + 2^-(sh+1)) for sh >= 1; for sh <= 0 the scaled value is an integer
         const double sc = ldexp(1.0, -g.sh2), half = g.sh2 >= 1 ? ldexp(0.5, -g.sh2) : 0.0;
+        // 16-bit table entries times 16-bit up values: |silu up| < 2^30, so for shifts 1..30 the
+        // product, its rounding offset and the shift stay in int32 (one 24-bit multiply)
+        const int32_t rnd2 = EPI == EPI_SILU_I ? 1 << (g.sh2 - 1) : 0;
         const size_t pl = (size_t)g.M * (N / 2);
         // gated columns nb BN / 2 + 32 wn .. + 31: K block (nb BN / 2 + 32 wn) / 64, offset 32 (wn % 2)
         uint8_t* tb = (uint8_t*)g.out + (size_t)(nb * (C::BN / 128) + (wn >> 1)) * g.M * 64 + (size_t)m0 * 64;
         const uint32_t lane_b4 = (uint32_t)(rw + (fc & 3)) * 64u + (uint32_t)((wn & 1) * 32 + (fc & ~3));
+        // limb bytes (the low bytes carry the -128 bias, the top byte is signed) of rows r = 0..3 of
+        // each 4-row group, then a 4 x 4 byte transpose across the lanes of a quad: lane j of the
+        // quad ends with row j, columns 4 (fc / 4) .. + 3, one dword per plane
+        const uint32_t xb = g.bits2 == 16 ? 0x80u : 0x808080u;
+        const uint32_t sel1 = (lane & 1) ? 0x03070105u : 0x06020400u;
+        const uint32_t sel2 = (lane & 2) ? 0x03020706u : 0x05040100u;
+        auto tr4 = [&](uint32_t w) __attribute__((always_inline)) {
+          uint32_t x = (uint32_t)__builtin_amdgcn_mov_dpp((int)w, 0xB1, 0xF, 0xF, false);
+          w = __builtin_amdgcn_perm(x, w, sel1);
+          x = (uint32_t)__builtin_amdgcn_mov_dpp((int)w, 0x4E, 0xF, 0xF, false);
+          return __builtin_amdgcn_perm(x, w, sel2);
+        };
 #pragma unroll
         for (int tm = 0; tm < C::TM; ++tm) {
-          int32_t gv[16], sv[16];
-          double uv[16];
 #pragma unroll
-          for (int e = 0; e < 16; ++e) { gv[e] = value16(tm, 0, e); uv[e] = value16d(tm, 1, e); }
-          // SiLU table reads: gates within the LDS window read it there, the others global memory
-          // (32-bit offsets from the table base; lanes served by LDS point at one shared line)
-          bool inw[16];
+          for (int b = 0; b < 4; ++b) {   // rows 8 b + 4 h + 0..3 of the 32-row tile tm
+            int32_t gv[4], sv[4], ui[4], vv[4];
 #pragma unroll
-          for (int e = 0; e < 16; ++e) {
-            const int wi = gv[e] + tab_half;
-            inw[e] = (uint32_t)wi < (uint32_t)(2 * tab_half);
-            sv[e] = tabw[min(max(wi, 0), 2 * kTabHalf - 1)];
-          }
+            for (int r = 0; r < 4; ++r) { gv[r] = value16(tm, 0, 4 * b + r); ui[r] = value16(tm, 1, 4 * b + r); }
+            // SiLU table reads: gates within the LDS window read it there; the others read global
+            // memory, only in the groups of 64 gates where some lane needs it (32-bit offsets from
+            // the table base; lanes served by LDS point at one shared line)
+            bool inw[4];
 #pragma unroll
-          for (int e = 0; e < 16; ++e) {
-            const int32_t t = *(const int32_t*)((const char*)g.aux_tab + (uint32_t)(inw[e] ? 32768 : gv[e] + 32768) * 4u);
-            if (!inw[e]) sv[e] = t;
-          }
-          int32_t vv[16];
+            for (int r = 0; r < 4; ++r) {
+              const int wi = gv[r] + tab_half;
+              inw[r] = (uint32_t)wi < (uint32_t)(2 * tab_half);
+              sv[r] = tabw[min(max(wi, 0), 2 * kTabHalf - 1)];
+            }
 #pragma unroll
-          for (int e = 0; e < 16; ++e) {
-            // SAT(RS(silu * up, sh2), bits2): the product and the scaled sum are exact in float64
-            const double x = (double)sv[e] * uv[e];
-            vv[e] = rne_i32(fmin(fmax(fma(x, sc, half), lo), hi));
-          }
-          // limb bytes (the low bytes carry the -128 bias, the top byte is signed) of rows
-          // r = 0..3 of each 4-row group, then a 4 x 4 byte transpose across the lanes of a quad:
-          // lane j of the quad ends with row j, columns 4 (fc / 4) .. + 3, one dword per plane
-          const uint32_t xb = g.bits2 == 16 ? 0x80u : 0x808080u;
-          const uint32_t sel1 = (lane & 1) ? 0x03070105u : 0x06020400u;
-          const uint32_t sel2 = (lane & 2) ? 0x03020706u : 0x05040100u;
-          auto tr4 = [&](uint32_t w) __attribute__((always_inline)) {
-            uint32_t x = (uint32_t)__builtin_amdgcn_mov_dpp((int)w, 0xB1, 0xF, 0xF, false);
-            w = __builtin_amdgcn_perm(x, w, sel1);
-            x = (uint32_t)__builtin_amdgcn_mov_dpp((int)w, 0x4E, 0xF, 0xF, false);
-            return __builtin_amdgcn_perm(x, w, sel2);
-          };
+            for (int r = 0; r < 4; ++r) {
+              const int32_t t = *(const int32_t*)((const char*)g.aux_tab + (uint32_t)(inw[r] ? 32768 : gv[r] + 32768) * 4u);
+              if (!inw[r]) sv[r] = t;
+            }
 #pragma unroll
-          for (int b = 0; b < 4; ++b) {
-            const uint32_t v0 = (uint32_t)vv[4 * b] ^ xb, v1 = (uint32_t)vv[4 * b + 1] ^ xb;
-            const uint32_t v2 = (uint32_t)vv[4 * b + 2] ^ xb, v3 = (uint32_t)vv[4 * b + 3] ^ xb;
+            for (int r = 0; r < 4; ++r) {
+              if constexpr (EPI == EPI_SILU_I) {
+                // SAT(RS(silu * up, sh2), bits2) in int32 (|silu up| < 2^30, sh2 in 1..30)
+                const int32_t q = (__mul24(sv[r], ui[r]) + rnd2) >> g.sh2;
+                vv[r] = g.bits2 == 16 ? min(max(q, -32768), 32767) : q;
+              } else {
+                // the product and the scaled sum are exact in float64
+                vv[r] = rne_i32(fmin(fmax(fma((double)sv[r] * (double)ui[r], sc, half), lo), hi));
+              }
+            }
+            const uint32_t v0 = (uint32_t)vv[0] ^ xb, v1 = (uint32_t)vv[1] ^ xb;
+            const uint32_t v2 = (uint32_t)vv[2] ^ xb, v3 = (uint32_t)vv[3] ^ xb;
             const uint32_t t01 = __builtin_amdgcn_perm(v1, v0, 0x05010400u), t23 = __builtin_amdgcn_perm(v3, v2, 0x05010400u);
             const uint32_t p0 = tr4(__builtin_amdgcn_perm(t23, t01, 0x05040100u));
             const uint32_t p1 = tr4(__builtin_amdgcn_perm(t23, t01, 0x07060302u));
@@ -1452,7 +1462,9 @@ hipError_t gemm(const GemmArgs& a, int a_bytes, int epi, hipStream_t s) {
     case EPI_REQ32: return launch_gemm<AW, EPI_REQ32>(a, s);             \
     case EPI_RESID: return launch_gemm<AW, EPI_RESID>(a, s);             \
     case EPI_LOGITS: return launch_gemm<AW, EPI_LOGITS>(a, s);           \
-    case EPI_SILU: return launch_gemm<AW, EPI_SILU>(a, s);               \
+    case EPI_SILU:                                                       \
+      if (a.tab_bits == 16 && a.sh2 >= 1 && a.sh2 <= 30) return launch_gemm<AW, EPI_SILU_I>(a, s); \
+      return launch_gemm<AW, EPI_SILU>(a, s);                             \
     case EPI_QKV: return launch_gemm<AW, EPI_QKV>(a, s);                 \
   }
   if (a_bytes == 2) { EII_EPIS(2) }

@@ -309,6 +309,8 @@ def main():
     ap.add_argument("--decode", action="store_true",
                     help="time KV-cached decoding instead: the configuration's sequences minus their last "
                          "--steps tokens as the prompt, then --steps single-token appends (one JSON line)")
+    ap.add_argument("--graphs", choices=("on", "off", "auto"), default="auto",
+                    help="replay each forward as a HIP graph (auto: on for the 1 x 128 latency configuration)")
     ap.add_argument("--cpu-numpy-leg", nargs=2, metavar=("MODEL", "IDS"), help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.cpu_numpy_leg:
@@ -350,21 +352,30 @@ def main():
         L.check(lib.eii_forward(eng.h, C.c_void_p(ids.data_ptr()), B, T, None, None,
                                 C.c_void_p(logits.data_ptr()), None, stream))
 
+    graphs = args.graphs == "on" or (args.graphs == "auto" and args.config == "cfg3")
+    eng.set_graphs(graphs)
     for _ in range(args.warmup):
         step()
     eng.check()
     torch.cuda.synchronize()
 
+    # per-launch HIP events on the launch stream (plain launches): over the timed steps, or, when the
+    # timed steps replay graphs, over as many steps again right after them
     launches_per_step = 1 + NL * 9 + 2
-    L.check(lib.eii_profile_begin(eng.h, launches_per_step * args.steps + 16))
+    ms = (C.c_double * len(L.KERNEL_KINDS))()
+    cnt = (C.c_int * len(L.KERNEL_KINDS))()
+    if not graphs:
+        L.check(lib.eii_profile_begin(eng.h, launches_per_step * args.steps + 16))
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
         step()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    ms = (C.c_double * len(L.KERNEL_KINDS))()
-    cnt = (C.c_int * len(L.KERNEL_KINDS))()
+    if graphs:
+        L.check(lib.eii_profile_begin(eng.h, launches_per_step * args.steps + 16))
+        for _ in range(args.steps):
+            step()
     L.check(lib.eii_profile_end(eng.h, stream, ms, cnt))
     eng.check()
     per_kind = {k: {"ms_total": ms[i], "launches": cnt[i]} for i, k in enumerate(L.KERNEL_KINDS)}
@@ -451,6 +462,10 @@ def main():
         "forward_ops_per_token_algorithmic": fwd_alg_ops / M,
         "forward_mfma_frac_limb_weighted": fwd_mfma_ops / (elapsed / args.steps) / PEAK_INT8_OPS,
         "kernels_ms_per_step": {k: v["ms_total"] / args.steps for k, v in per_kind.items()},
+        "hip_graphs": graphs,
+        "kernels_timing": ("per-launch HIP events over the timed steps" if not graphs else
+                           "per-launch HIP events over an equal number of plain-launch steps after the timed "
+                           "graph replays"),
         "cpu_baseline": cpu,
     }
     print(json.dumps(res))

@@ -112,6 +112,19 @@ struct eii_model {
   std::vector<hipEvent_t> ev;      // start/stop pairs
   std::vector<int> ev_kind;
   size_t ev_used = 0;
+  // HIP graphs of whole forwards (eii_model_set_graphs): captured on an internal stream the first
+  // time a batch shape and set of output buffers is seen, replayed on the caller's stream after.
+  // The graphs hold the workspace and table addresses, so growing the workspace or replacing the
+  // RoPE tables drops them.
+  struct FwdGraph {
+    std::vector<int32_t> lens;
+    const void *ids, *emb, *res, *lg;
+    std::vector<uint8_t> mask;
+    hipGraphExec_t exec;
+  };
+  bool graphs = false;
+  hipStream_t cap_stream = nullptr;
+  std::vector<FwdGraph> fwd_graphs;
 };
 
 // KV cache of incremental decoding: per layer the q|k|v rows (int16 [B cap][960], row b cap + t
@@ -446,9 +459,16 @@ static void free_ws(eii_model* m) {
   m->ws_rows = 0;
 }
 
+static void drop_graphs(eii_model* m) {
+  for (auto& gr : m->fwd_graphs) (void)hipGraphExecDestroy(gr.exec);
+  m->fwd_graphs.clear();
+}
+
 extern "C" void eii_model_free(eii_model* m) {
   if (!m) return;
   (void)hipSetDevice(m->device);
+  drop_graphs(m);
+  if (m->cap_stream) (void)hipStreamDestroy(m->cap_stream);
   free_ws(m);
   if (m->seq_off) (void)hipFree(m->seq_off);
   if (m->rope_owned) { (void)hipFree(m->rope_c); (void)hipFree(m->rope_s); }
@@ -478,6 +498,7 @@ extern "C" int eii_model_set_rope(eii_model* m, const int64_t* c, const int64_t*
     return fail(EII_E_DEVICE, "rope upload");
   }
   if (m->rope_owned) { (void)hipFree(m->rope_c); (void)hipFree(m->rope_s); }
+  drop_graphs(m);
   m->rope_c = dc;
   m->rope_s = ds;
   m->rope_rows = rows;
@@ -499,6 +520,7 @@ namespace {
 
 int ensure_ws(eii_model* m, size_t rows) {
   if (rows <= m->ws_rows) return EII_OK;
+  drop_graphs(m);
   free_ws(m);
   size_t r = rows;
   hipError_t e = hipSuccess;
@@ -720,6 +742,43 @@ int forward_impl(eii_model* m, const int64_t* ids, const std::vector<int32_t>& l
   HIPCHK(hipSetDevice(m->device));
   int rc;
   if ((rc = ensure_ws(m, M)) || (rc = set_batch(m, lens, s))) return rc;
+  if (m->graphs && !m->prof) {
+    // replay the graph of this shape and these buffers, or capture it now (the positions and
+    // sequence offsets it reads were uploaded by set_batch above, outside the graph)
+    std::vector<uint8_t> mask;
+    if (dump_mask) mask.assign(dump_mask, dump_mask + lens.size());
+    for (auto& gr : m->fwd_graphs)
+      if (gr.lens == lens && gr.ids == ids && gr.emb == emb_out && gr.res == res_out && gr.lg == logits &&
+          gr.mask == mask) {
+        HIPCHK(hipGraphLaunch(gr.exec, s));
+        return EII_OK;
+      }
+    // capture records without running anything (the legacy default stream cannot be captured, so
+    // an internal stream records); the replay below is ordered on the caller's stream
+    if (!m->cap_stream) HIPCHK(hipStreamCreateWithFlags(&m->cap_stream, hipStreamNonBlocking));
+    HIPCHK(hipStreamBeginCapture(m->cap_stream, hipStreamCaptureModeThreadLocal));
+    m->graphs = false;   // the launches below are recorded, not replayed
+    rc = forward_impl(m, ids, lens, emb_out, res_out, logits, dump_mask, m->cap_stream);
+    m->graphs = true;
+    hipGraph_t graph = nullptr;
+    const hipError_t ec = hipStreamEndCapture(m->cap_stream, &graph);
+    if (rc) {
+      if (graph) (void)hipGraphDestroy(graph);
+      return rc;
+    }
+    if (ec != hipSuccess) return fail(EII_E_DEVICE, std::string("graph capture: ") + hipGetErrorString(ec));
+    hipGraphExec_t exec = nullptr;
+    const hipError_t ei = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (ei != hipSuccess) return fail(EII_E_DEVICE, std::string("graph instantiate: ") + hipGetErrorString(ei));
+    if (m->fwd_graphs.size() >= 8) {   // a few shapes at a time
+      (void)hipGraphExecDestroy(m->fwd_graphs.front().exec);
+      m->fwd_graphs.erase(m->fwd_graphs.begin());
+    }
+    m->fwd_graphs.push_back({lens, ids, emb_out, res_out, logits, mask, exec});
+    HIPCHK(hipGraphLaunch(exec, s));
+    return EII_OK;
+  }
   const int Mi = (int)M;
   const std::vector<DumpRun> runs = dump_runs(lens, dump_mask);
   size_t dump_rows = 0;
@@ -745,6 +804,16 @@ int forward_impl(eii_model* m, const int64_t* ids, const std::vector<int32_t>& l
 }
 
 }  // namespace
+
+extern "C" int eii_model_set_graphs(eii_model* m, int on) {
+  if (!m) return fail(EII_E_ARG, "null model");
+  if (!on) {
+    HIPCHK(hipSetDevice(m->device));
+    drop_graphs(m);
+  }
+  m->graphs = on != 0;
+  return EII_OK;
+}
 
 extern "C" int eii_forward(eii_model* m, const int64_t* ids, int B, int T, int32_t* emb_out, int32_t* res_out,
                            int32_t* logits, const uint8_t* dump_mask, void* stream) {

@@ -68,6 +68,10 @@ class Engine:
         L.check(self.lib.eii_model_formats(self.h, layer, fm.ctypes.data_as(L.i64p), fy.ctypes.data_as(L.i64p)))
         return fm, int(fy[0])
 
+    def set_graphs(self, on=True):
+        """Replay whole forwards as HIP graphs (captured per batch shape and output buffers)."""
+        L.check(self.lib.eii_model_set_graphs(self.h, 1 if on else 0))
+
     def ensure_rope(self, T):
         if T > self.rope_rows:
             self.set_rope(max(T, 2 * self.rope_rows))

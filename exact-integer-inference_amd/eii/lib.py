@@ -41,6 +41,7 @@ SIGNATURES = {
     "eii_model_set_rope": (i32, [vp, i64p, i64p, i32]),
     "eii_model_rope_rows": (i32, [vp]),
     "eii_model_formats": (i32, [vp, i32, i64p, i64p]),
+    "eii_model_set_graphs": (i32, [vp, i32]),
     "eii_forward": (i32, [vp, vp, i32, i32, vp, vp, vp, vp, vp]),
     "eii_forward_packed": (i32, [vp, vp, i32p, i32, vp, vp, vp, vp, vp]),
     "eii_check": (i32, [vp, vp]),

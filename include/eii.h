@@ -77,6 +77,13 @@ int eii_forward_packed(eii_model* m, const int64_t* ids_dev, const int32_t* seq_
                        int32_t* embed_out_dev, int32_t* resid_out_dev, int32_t* logits_dev,
                        const uint8_t* dump_mask_host, void* stream);
 
+/* Run eii_forward / eii_forward_packed as HIP graphs (on != 0) or as individual launches (0, the
+ * default).  With graphs on, the first call for a batch shape and set of buffer pointers (ids,
+ * outputs, dump mask) captures the forward's launches into a graph and replays it on `stream`;
+ * later calls with the same shape and pointers replay that graph (no host work per kernel).  Growing the workspace or replacing the RoPE tables drops the graphs; profiling
+ * (eii_profile_begin) runs the plain launches.  No counterpart in the reference. */
+int eii_model_set_graphs(eii_model* m, int on);
+
 /* Waits for `stream`, then reports data-dependent violations seen since the last check:
  * a token id outside [0, 49152) or a logit outside int32 (status 4). */
 int eii_check(eii_model* m, void* stream);

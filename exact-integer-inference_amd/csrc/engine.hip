@@ -644,13 +644,13 @@ int run_block(eii_model* m, int l, int32_t* x, int M, int nseq, int max_T, const
     HIPCHK(attention(a, s));
   }
   // traces: RS(acc m, n + f_c - 15) before the saturating add, from the exact int64 accumulators
-  auto res_update = [&](const Mat& W, const void* planes, int planes_n, int64_t* out) -> int {
-    HIPCHK(gemm_i64_anyk((const uint8_t*)planes, planes_n, W.Wf, W.wsum, M, W.N, W.K, out, s));
+  auto res_update = [&](const Mat& W, const void* planes, int planes_n, int64_t* out, int a_kb) -> int {
+    HIPCHK(gemm_i64_anyk((const uint8_t*)planes, planes_n, W.Wf, W.wsum, M, W.N, W.K, out, s, a_kb));
     HIPCHK(requant_i64(out, M, W.N, W.mult, W.shift, 64, out, s));
     return EII_OK;
   };
   int rc;
-  if (tr && tr->o_res && (rc = res_update(L.o, m->ctx, cb, tr->o_res))) return rc;
+  if (tr && tr->o_res && (rc = res_update(L.o, m->ctx, cb, tr->o_res, 64))) return rc;
   {
     ProfScope ps(m, EII_K_GEMM_O, s);
     HIPCHK(gemm(gemm_args(L.o, m->ctx, M, x, 32), cb, EPI_RESID, s));
@@ -682,11 +682,13 @@ int run_block(eii_model* m, int l, int32_t* x, int M, int nseq, int max_T, const
       HIPCHK(hipMemcpy2DAsync(tr->up_proj, 64, (const uint8_t*)m->gu + 64, 128, 64, (size_t)M * 48,
                               hipMemcpyDeviceToDevice, s));
     HIPCHK(silu_gate(m->gu, M, L.silu, sh_s, L.bits[GATED], (uint8_t*)m->gated, tr->mlp_gated, s, tr->silu_gate));
-    if (tr->down_res && (rc = res_update(L.down, m->gated, gb, tr->down_res))) return rc;
+    if (tr->down_res && (rc = res_update(L.down, m->gated, gb, tr->down_res, 32))) return rc;
   }
   {
     ProfScope ps(m, EII_K_GEMM_DOWN, s);
-    HIPCHK(gemm(gemm_args(L.down, m->gated, M, x, 32), gb, EPI_RESID, s));
+    GemmArgs g = gemm_args(L.down, m->gated, M, x, 32);
+    g.a_kb = 32;   // the gated planes' 32-byte K blocks
+    HIPCHK(gemm(g, gb, EPI_RESID, s));
   }
   return EII_OK;
 }

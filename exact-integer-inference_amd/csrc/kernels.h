@@ -30,6 +30,13 @@ enum Epi : int {
 __host__ __device__ inline size_t plane_offset(size_t m, size_t k, size_t M) {
   return (k >> 6) * M * 64 + m * 64 + (k & 63);
 }
+// The gated MLP activations (the SiLU-gate product, input of the down projection) use 32-byte K
+// blocks instead, [K / 32][M][32]: the gate/up epilogue then writes 4 consecutive rows x 32 gated
+// columns of a wave as one whole 128-byte line (no partially written lines, whose write-back
+// costs a fill from memory).  K block b of 64 bytes still starts at byte b M 64.
+__host__ __device__ inline size_t plane_offset32(size_t m, size_t k, size_t M) {
+  return (k >> 5) * M * 32 + m * 32 + (k & 31);
+}
 // Weights enter the GEMM in MFMA fragment order (swizzle_weights): for each block of 32 output
 // rows and each 32-column K slice, the 64 lanes' 16-byte operands in lane order,
 // [ceil(N / 32)][K / 32][64][16] (lane 32 h + c: row 32 b + c, columns 16 h .. 16 h + 15 of
@@ -69,6 +76,8 @@ struct GemmArgs {
   // EPI_I64 only: add the accumulators to the int64 values already in out (K-range passes after
   // the first); wsum may be null, meaning no limb bias term (the first pass adds it for all of K)
   bool accumulate = false;
+  // K-block width of the activation planes in bytes: 64 (plane_offset) or 32 (plane_offset32)
+  int a_kb = 64;
 };
 
 // V^T limb planes for attention: plane 0 = low bytes - 128, plane 1 = signed high bytes of v;
@@ -82,9 +91,10 @@ hipError_t build_vt(const int16_t* qkv, int M, uint8_t* vt, hipStream_t s);
 hipError_t gemm(const GemmArgs& a, int a_bytes, int epi, hipStream_t s);
 // Exact int64 out [M, N] = A W^T for any K: A as limb planes of K rounded up to a multiple of 64
 // (a_bytes 2 or 4), W in fragment order over the same padded K (zero columns past K), wsum [N];
-// the K blocks run in passes of the GEMM's compiled K-block counts, accumulated in out.
+// the K blocks run in passes of the GEMM's compiled K-block counts, accumulated in out.  a_kb: the
+// planes' K-block width (GemmArgs::a_kb).
 hipError_t gemm_i64_anyk(const uint8_t* planes, int a_bytes, const int8_t* Wf, const int32_t* wsum, int M, int N,
-                         int Kp, int64_t* out, hipStream_t s);
+                         int Kp, int64_t* out, hipStream_t s, int a_kb = 64);
 // out [M, N] (int16, int32 or int64 by out_bits; 64 = no saturation) = SAT(RS(acc * mult[n], shift[n]), out_bits)
 // from exact int64 (in place when out == acc)
 // accumulators (python/intref.py:189), in int64 as the reference
@@ -118,7 +128,8 @@ hipError_t rope(int16_t* qkv, int M, const int32_t* pos, const int32_t* cosT, co
 
 // gated[m, j] = SAT(RS(silu[gate + 32768] * up, sh), bits) with gu rows holding [gate 32 | up 32]
 // blocks: gate j at column 64 (j / 32) + j % 32, up j 32 columns further
-// sg_out int32 [M, 1536] (nullable, traces): the table values silu[gate + 32768]
+// sg_out int32 [M, 1536] (nullable, traces): the table values silu[gate + 32768]; planes (nullable)
+// in the 32-byte K-block layout (plane_offset32), as the fused gate/up epilogue writes them
 hipError_t silu_gate(const int16_t* gu, int M, const int32_t* silu, int sh, int bits,
                      uint8_t* planes, void* plain, hipStream_t s, int32_t* sg_out = nullptr);
 // Trace of attention's scores and probabilities for B sequences of T rows each (see kernels.hip)

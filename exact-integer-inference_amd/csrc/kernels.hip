@@ -191,8 +191,11 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
     for (int i = 0; i < C::kAChunks; ++i) {
       // LDS slot q (16 bytes) of the stage: limb plane l, row, physical chunk cp
       const int q = tid + C::kThreads * i, l = q / (4 * C::BM), row = (q >> 2) % C::BM, cp = q & 3;
-      const int m = min(m0 + row, g.M - 1);
-      a_src[i] = Ab + (size_t)l * g.a_plane + (size_t)m * 64 + lds_swz(row, cp) * 16;
+      const int m = min(m0 + row, g.M - 1), c = lds_swz(row, cp);
+      // 16-byte chunk c of the K block: bytes 16 c of a 64-byte row, or 16 (c & 1) of the row in
+      // 32-byte block c >> 1
+      a_src[i] = Ab + (size_t)l * g.a_plane +
+                 (g.a_kb == 32 ? (size_t)(c >> 1) * g.M * 32 + (size_t)m * 32 + (c & 1) * 16 : (size_t)m * 64 + c * 16);
     }
   };
   auto point_w = [&](int nb) __attribute__((always_inline)) {
@@ -398,8 +401,8 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
         else return (double)value16(tm, tn, e);
       };
       if constexpr (kSilu) {
-        // gated limb planes (bits2 / 8 planes of M x N / 2, K-blocked): the lane's gated column
-        // n0 / 2 + wn 32 + fc lies in 64-column block nb at offset wn 32 + fc
+        // gated limb planes (bits2 / 8 planes of M x N / 2 in 32-byte K blocks, plane_offset32): the
+        // lane's gated column n0 / 2 + wn 32 + fc is column fc of 32-column block nb BN / 64 + wn
         const double lo = -ldexp(1.0, g.bits2 - 1), hi = ldexp(1.0, g.bits2 - 1) - 1.0;
         // RS(x, sh) = RNE(x 2^-sh + 2^-(sh+1)) for sh >= 1; for sh <= 0 the scaled value is an integer
         const double sc = ldexp(1.0, -g.sh2), half = g.sh2 >= 1 ? ldexp(0.5, -g.sh2) : 0.0;
@@ -407,9 +410,10 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
         // product, its rounding offset and the shift stay in int32 (one 24-bit multiply)
         const int32_t rnd2 = EPI == EPI_SILU_I ? 1 << (g.sh2 - 1) : 0;
         const size_t pl = (size_t)g.M * (N / 2);
-        // gated columns nb BN / 2 + 32 wn .. + 31: K block (nb BN / 2 + 32 wn) / 64, offset 32 (wn % 2)
-        uint8_t* tb = (uint8_t*)g.out + (size_t)(nb * (C::BN / 128) + (wn >> 1)) * g.M * 64 + (size_t)m0 * 64;
-        const uint32_t lane_b4 = (uint32_t)(rw + (fc & 3)) * 64u + (uint32_t)((wn & 1) * 32 + (fc & ~3));
+        // the 4 lanes of a quad hold 4 consecutive rows and the 8 quads of a half-wave the block's 32
+        // columns, so each half-wave store covers one 128-byte line (4 rows x 32 bytes)
+        uint8_t* tb = (uint8_t*)g.out + (size_t)(nb * (C::BN / 64) + wn) * g.M * 32 + (size_t)m0 * 32;
+        const uint32_t lane_b4 = (uint32_t)(rw + (fc & 3)) * 32u + (uint32_t)(fc & ~3);
         // limb bytes (the low bytes carry the -128 bias, the top byte is signed) of rows r = 0..3 of
         // each 4-row group, then a 4 x 4 byte transpose across the lanes of a quad: lane j of the
         // quad ends with row j, columns 4 (fc / 4) .. + 3, one dword per plane
@@ -468,7 +472,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
             }
             const int row = 32 * tm + 8 * b;   // + the lane's rw + (fc & 3)
             if (!full && m0 + rw + (fc & 3) + row >= g.M) continue;
-            uint32_t* ob = (uint32_t*)(tb + (size_t)row * 64 + lane_b4);
+            uint32_t* ob = (uint32_t*)(tb + (size_t)row * 32 + lane_b4);
             ob[0] = p0;
             *(uint32_t*)((uint8_t*)ob + pl) = p1;
             if (g.bits2 != 16) {
@@ -893,7 +897,7 @@ __global__ __launch_bounds__(256) void silu_kernel(const int16_t* gu, int M, con
   if (sg_out) sg_out[t] = silu[g + 32768];
   if (planes) {
 #pragma unroll
-    for (int l = 0; l < OB; ++l) planes[l * (size_t)M * kDFF + plane_offset(row, j, M)] = (uint8_t)limb_byte(o, l, OB);
+    for (int l = 0; l < OB; ++l) planes[l * (size_t)M * kDFF + plane_offset32(row, j, M)] = (uint8_t)limb_byte(o, l, OB);
   }
   if (plain) {
     if constexpr (OB == 2) ((int16_t*)plain)[t] = (int16_t)o;
@@ -1528,7 +1532,7 @@ hipError_t swizzle_weights(const int8_t* W, int N, int K, int8_t* Wf, hipStream_
 }
 
 hipError_t gemm_i64_anyk(const uint8_t* planes, int a_bytes, const int8_t* Wf, const int32_t* wsum, int M, int N,
-                         int Kp, int64_t* out, hipStream_t s) {
+                         int Kp, int64_t* out, hipStream_t s, int a_kb) {
   if (Kp <= 0 || Kp % kBK != 0) return hipErrorInvalidValue;
   // passes over ranges of the K blocks, each a compiled K-block count (24, 9, 2 or 1), largest first
   int b0 = 0;
@@ -1539,6 +1543,7 @@ hipError_t gemm_i64_anyk(const uint8_t* planes, int a_bytes, const int8_t* Wf, c
                b0 == 0 ? wsum : nullptr, nullptr, nullptr, out, 64, nullptr};
     g.w_ld = Kp;
     g.accumulate = b0 > 0;
+    g.a_kb = a_kb;   // K block b0 (64 bytes) starts at byte b0 M 64 in both layouts
     const hipError_t e = gemm(g, a_bytes, EPI_I64, s);
     if (e != hipSuccess) return e;
     b0 += nb;

@@ -78,6 +78,8 @@ struct GemmArgs {
   bool accumulate = false;
   // K-block width of the activation planes in bytes: 64 (plane_offset) or 32 (plane_offset32)
   int a_kb = 64;
+  // row blocks per group of the tile order (set by the launch)
+  int tile_g = 8;
 };
 
 // V^T limb planes for attention: plane 0 = low bytes - 128, plane 1 = signed high bytes of v;

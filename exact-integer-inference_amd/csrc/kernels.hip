@@ -116,12 +116,18 @@ struct GemmCfg {
   static_assert(kAChunks * kThreads == AW * BM * 4, "chunk split");
 };
 
-// Tiles in grouped order: 8 row blocks x all column blocks per group.  Each XCD (= blockIdx % 8,
+// Tiles in grouped order: G row blocks x all column blocks per group.  Each XCD (= blockIdx % 8,
 // the hardware's round-robin dispatch) owns a contiguous range of that order, and the persistent
 // workgroups of one XCD sweep it together, so concurrently running tiles of an XCD share
-// activation rows and weight blocks in its L2.
-__device__ __forceinline__ void tile_coords(int v, int nMB, int nNB, int& mb, int& nb) {
-  const int G = 8, grp = v / (G * nNB), first = grp * G;
+// activation rows and weight blocks in its L2.  G = 1 (row-major order) for K <= 576 when the
+// whole weight matrix fits the L2 beside the operand stream (q/k/v, o, gate/up): the column tiles
+// of a row block then run at the same time and read each activation K block once, where with
+// G = 8 the 64 tiles an XCD runs at a time cover only part of a group's columns and the rest fetch
+// the same rows again later (gate/up at 256 x 160 tokens: 162 -> 92 MB fetched per launch).  G = 8
+// for the head, whose weights (28 MB) do not fit (8 row blocks share each weight block), and for
+// the 1536-deep down projection, which row-major order made 3 % slower although it fetched less.
+__device__ __forceinline__ void tile_coords(int v, int nMB, int nNB, int G, int& mb, int& nb) {
+  const int grp = v / (G * nNB), first = grp * G;
   const int gs = min(nMB - first, G), in = v - grp * G * nNB;
   mb = first + in % gs;
   nb = in / gs;
@@ -183,7 +189,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
   const uint8_t* a_src[C::kAChunks];
   const int8_t* w_src[C::TN];
   auto coords = [&](int j, int& mb, int& nb) __attribute__((always_inline)) {
-    tile_coords(v0 + min(j, ntiles - 1) * nwg_x, nMB, nNB, mb, nb);
+    tile_coords(v0 + min(j, ntiles - 1) * nwg_x, nMB, nNB, g.tile_g, mb, nb);
   };
   auto point_a = [&](int mb) __attribute__((always_inline)) {
     const int m0 = mb * C::BM;
@@ -192,10 +198,10 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
       // LDS slot q (16 bytes) of the stage: limb plane l, row, physical chunk cp
       const int q = tid + C::kThreads * i, l = q / (4 * C::BM), row = (q >> 2) % C::BM, cp = q & 3;
       const int m = min(m0 + row, g.M - 1), c = lds_swz(row, cp);
-      // 16-byte chunk c of the K block: bytes 16 c of a 64-byte row, or 16 (c & 1) of the row in
-      // 32-byte block c >> 1
-      a_src[i] = Ab + (size_t)l * g.a_plane +
-                 (g.a_kb == 32 ? (size_t)(c >> 1) * g.M * 32 + (size_t)m * 32 + (c & 1) * 16 : (size_t)m * 64 + c * 16);
+      // 16-byte chunk c of the K block: bytes 16 c of a 64-byte row (a_kb 64), or bytes 16 (c & 1)
+      // of the row in 32-byte block c >> 1 (a_kb 32)
+      const int cb = g.a_kb >> 4;   // chunks per row of a block: 4 or 2
+      a_src[i] = Ab + (size_t)l * g.a_plane + (size_t)(c / cb) * g.M * g.a_kb + (uint32_t)(m * g.a_kb + (c % cb) * 16);
     }
   };
   auto point_w = [&](int nb) __attribute__((always_inline)) {
@@ -660,8 +666,10 @@ int device_cus() {
 }
 
 template <int AW, int EPI, int SHAPE>
-hipError_t launch_gemm_cfg(const GemmArgs& a, hipStream_t s) {
+hipError_t launch_gemm_cfg(const GemmArgs& a_in, hipStream_t s) {
   using C = GemmCfg<AW, SHAPE>;
+  GemmArgs a = a_in;
+  a.tile_g = (size_t)a.N * a.K <= ((size_t)1 << 21) && a.K <= 576 ? 1 : 8;   // see tile_coords
   const int nT = ((a.M + C::BM - 1) / C::BM) * ((a.N + C::BN - 1) / C::BN);
   // two persistent workgroups per CU, a multiple of 8 so every XCD gets the same count
   const int per_xcd = std::min((nT + 7) / 8, std::max(1, 2 * device_cus() / 8));

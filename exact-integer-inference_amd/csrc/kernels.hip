@@ -98,20 +98,29 @@ __device__ __forceinline__ v16i mfma32(v4i a, v4i b, v16i c) {
 //     no half-empty ones), 2-limb activations only;
 //   kShapeRow: 1 x 4 waves, 64 x 256 tiles for wide 2-limb GEMMs (q/k/v, gate/up, the head): the four
 //     waves share one 64-row activation tile in LDS (half the LDS traffic of a 128-row tile per MFMA
-//     column) and each loads its own weight columns.
-constexpr int kShapeSquare = 0, kShapeNarrow = 1, kShapeRow = 2;
+//     column) and each loads its own weight columns;
+//   kShapeSkinny: at most 32 rows (decoding steps): one 32 x 64 tile per workgroup, the K slices split
+//     over the 4 waves, every operand fragment loaded straight into registers at the start (one memory
+//     round trip instead of a pipelined K loop whose steps each wait for a weight load), the partial
+//     sums added through LDS, and wave 0 running the epilogue; many small tiles spread the weight
+//     reads over the CUs;
+//   kShapeSkinny32: the same with 32 x 32 tiles, for the epilogues without column pairs (twice the
+//     workgroups for the narrow residual GEMMs, N = 576).
+constexpr int kShapeSquare = 0, kShapeNarrow = 1, kShapeRow = 2, kShapeSkinny = 3, kShapeSkinny32 = 4;
 template <int AW, int SHAPE = kShapeSquare>
 struct GemmCfg {
-  static_assert(SHAPE == kShapeSquare || AW == 2, "narrow and row tiles for 2-limb activations");
+  static constexpr bool kSkinny = SHAPE == kShapeSkinny || SHAPE == kShapeSkinny32;
+  static_assert(SHAPE == kShapeSquare || kSkinny || AW == 2, "narrow and row tiles for 2-limb activations");
   static constexpr int kThreads = 256;                   // 4 waves; two workgroups share a CU
-  static constexpr int WGM = SHAPE == kShapeRow ? 1 : 2, WGN = 4 / WGM;   // wave grid
-  static constexpr int BM = SHAPE == kShapeSquare && AW == 2 ? 128 : 64;
-  static constexpr int BN = SHAPE == kShapeNarrow ? 192 : SHAPE == kShapeRow ? 256 : 128;
+  static constexpr int WGM = SHAPE == kShapeRow || kSkinny ? 1 : 2, WGN = kSkinny ? 1 : 4 / WGM;   // wave grid
+  static constexpr int BM = kSkinny ? 32 : SHAPE == kShapeSquare && AW == 2 ? 128 : 64;
+  static constexpr int BN = SHAPE == kShapeSkinny32 ? 32 : kSkinny ? 64 : SHAPE == kShapeNarrow ? 192 : SHAPE == kShapeRow ? 256 : 128;
   static constexpr int WM = BM / WGM, WN = BN / WGN;     // wave tile
   static constexpr int TM = WM / 32, TN = WN / 32;       // 32x32 tiles per wave
   static constexpr int kPlane = BM * kLdsRow;
-  static constexpr int kStage = AW * kPlane;              // activation limb planes only: 8 or 16 KB
-  static constexpr int kStages = 4;                       // loaded two and three steps ahead
+  // activation limb planes (8 or 16 KB per stage), or for kShapeSkinny the partial sums of waves 1..3
+  static constexpr int kStage = kSkinny ? 3 * TN * AW * 16 * 64 * 4 : AW * kPlane;
+  static constexpr int kStages = kSkinny ? 1 : 4;          // loaded two and three steps ahead
   static constexpr int kAChunks = AW * BM * 4 / kThreads;   // 16-byte direct-to-LDS loads per thread
   static_assert(kAChunks * kThreads == AW * BM * 4, "chunk split");
 };
@@ -136,7 +145,7 @@ __device__ __forceinline__ void tile_coords(int v, int nMB, int nNB, int G, int&
 __device__ __forceinline__ uint32_t pack16(int32_t a, int32_t b) { return (uint32_t)(a & 0xFFFF) | ((uint32_t)b << 16); }
 
 template <int AW, int EPI, int NK, int SHAPE>
-__global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
+__global__ __launch_bounds__(256, SHAPE == kShapeSkinny || SHAPE == kShapeSkinny32 ? 1 : 2) void gemm_kernel(GemmArgs g) {
   using C = GemmCfg<AW, SHAPE>;
   static_assert(SHAPE != kShapeNarrow || EPI == EPI_RESID || EPI == EPI_I64 || EPI == EPI_REQ16 ||
                 EPI == EPI_REQ32 || EPI == EPI_LOGITS,
@@ -151,16 +160,17 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
   constexpr int kTabBytes = kSilu ? 4 * kTabHalf : 0;
   __shared__ __attribute__((aligned(16))) uint8_t smem[C::kStages * C::kStage + kTabBytes];
   const int nMB = (g.M + C::BM - 1) / C::BM, nNB = (g.N + C::BN - 1) / C::BN, nT = nMB * nNB;
-  // this workgroup's tiles: v = v0, v0 + stride, ... < vend
-  const int xcd = blockIdx.x & 7, per = (nT + 7) / 8, nwg_x = gridDim.x >> 3;
-  const int v0 = xcd * per + (blockIdx.x >> 3), vend = min(nT, (xcd + 1) * per);
+  // this workgroup's tiles: v = v0, v0 + stride, ... < vend (kShapeSkinny: tile blockIdx.x alone)
+  const int xcd = blockIdx.x & 7, per = (nT + 7) / 8, nwg_x = C::kSkinny ? 1 : gridDim.x >> 3;
+  const int v0 = C::kSkinny ? (int)blockIdx.x : xcd * per + (blockIdx.x >> 3);
+  const int vend = C::kSkinny ? nT : min(nT, (xcd + 1) * per);
   if (v0 >= vend) return;
   const int ntiles = (vend - v0 + nwg_x - 1) / nwg_x;
   constexpr int nk = NK;
   int16_t* const tabw = (int16_t*)(smem + C::kStages * C::kStage);
   int tab_half = 0;   // 0: no LDS window (32-bit table), every read goes to global memory
   if constexpr (kSilu) {
-    if (g.tab_bits == 16) {
+    if (!C::kSkinny && g.tab_bits == 16) {   // (a skinny tile's few rows read the table in global memory)
       tab_half = kTabHalf;
       for (int i = threadIdx.x; i < 2 * kTabHalf; i += C::kThreads) tabw[i] = (int16_t)g.aux_tab[32768 - kTabHalf + i];
     }
@@ -567,6 +577,69 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
   // weights of s + 1 issued since.  Every tile is unrolled (two tiles per iteration when NK is
   // odd), so the register set of each step is a compile-time constant and a tile is straight-line
   // code up to its epilogue.
+  if constexpr (C::kSkinny) {
+    // tile v0 in row-major order; wave w takes the 32-wide K slices [2 NK w / 4, 2 NK (w + 1) / 4)
+    const int mb = v0 / nNB, nb = v0 % nNB;
+    constexpr int NS = 2 * NK, NSW = (NS + 3) / 4;
+    const int s0 = wave * NS / 4, cnt = (wave + 1) * NS / 4 - s0;
+    const int m = min(mb * C::BM + fc, g.M - 1), cb = g.a_kb >> 4;
+    const size_t wstride = (size_t)((g.w_ld ? g.w_ld : g.K) / 32) * 1024;
+    // fragments as in the LDS path: row fc, bytes 16 fh .. 16 fh + 15 of slice s (chunk c of its
+    // 64-byte K block in either plane layout); the weights of columns nb 64 + 32 tn + 0..31
+    v4i af[NSW][AW], wf[NSW][C::TN];
+#pragma unroll
+    for (int i = 0; i < NSW; ++i)
+      if (i < cnt) {
+        const int sl = s0 + i, c = 2 * (sl & 1) + fh;
+        const size_t aoff = (size_t)(sl >> 1) * g.M * 64 + (size_t)(c / cb) * g.M * g.a_kb + (uint32_t)(m * g.a_kb + (c % cb) * 16);
+#pragma unroll
+        for (int l = 0; l < AW; ++l) af[i][l] = *(const v4i*)(Ab + (size_t)l * g.a_plane + aoff);
+#pragma unroll
+        for (int tn = 0; tn < C::TN; ++tn) {
+          const int nb32 = min(nb * C::TN + tn, nb32_last);
+          wf[i][tn] = *(const v4i*)(g.W + (size_t)nb32 * wstride + (size_t)sl * 1024 + lane * 16);
+        }
+      }
+#pragma unroll
+    for (int i = 0; i < NSW; ++i)
+      if (i < cnt) {
+#pragma unroll
+        for (int l = 0; l < AW; ++l)
+#pragma unroll
+          for (int tn = 0; tn < C::TN; ++tn) acc[0][tn][l] = mfma32(af[i][l], wf[i][tn], acc[0][tn][l]);
+      }
+    // partial sums of waves 1..3 -> LDS as 16-byte groups [wave - 1][tn][l][e / 4][lane][e % 4];
+    // wave 0 adds them (each partial and the total are limb sums over part of K, below 2^31) and runs
+    // the epilogue
+    v4i* red = (v4i*)smem;
+    if (wave > 0) {
+#pragma unroll
+      for (int tn = 0; tn < C::TN; ++tn)
+#pragma unroll
+        for (int l = 0; l < AW; ++l)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            red[((((wave - 1) * C::TN + tn) * AW + l) * 4 + q) * 64 + lane] =
+                v4i{acc[0][tn][l][4 * q], acc[0][tn][l][4 * q + 1], acc[0][tn][l][4 * q + 2], acc[0][tn][l][4 * q + 3]};
+    }
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int w = 0; w < 3; ++w)
+#pragma unroll
+      for (int tn = 0; tn < C::TN; ++tn)
+#pragma unroll
+        for (int l = 0; l < AW; ++l)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const v4i p = red[(((w * C::TN + tn) * AW + l) * 4 + q) * 64 + lane];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[0][tn][l][4 * q + r] += p[r];
+          }
+    epilogue(mb, nb);
+    return;
+  }
+
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
   __builtin_amdgcn_s_setprio(kLoopPrio);
@@ -671,9 +744,10 @@ hipError_t launch_gemm_cfg(const GemmArgs& a_in, hipStream_t s) {
   GemmArgs a = a_in;
   a.tile_g = (size_t)a.N * a.K <= ((size_t)1 << 21) && a.K <= 576 ? 1 : 8;   // see tile_coords
   const int nT = ((a.M + C::BM - 1) / C::BM) * ((a.N + C::BN - 1) / C::BN);
-  // two persistent workgroups per CU, a multiple of 8 so every XCD gets the same count
+  // two persistent workgroups per CU, a multiple of 8 so every XCD gets the same count; one
+  // workgroup per tile for kShapeSkinny
   const int per_xcd = std::min((nT + 7) / 8, std::max(1, 2 * device_cus() / 8));
-  const dim3 grid(8 * per_xcd), block(C::kThreads);
+  const dim3 grid(C::kSkinny ? nT : 8 * per_xcd), block(C::kThreads);
   // K is a template parameter so each tile's K loop is straight-line code: the model's K
   // (576, 1536) for every epilogue, and 64, 128 for the operator entry points
   constexpr bool op = EPI == EPI_I64 || EPI == EPI_REQ16 || EPI == EPI_REQ32;
@@ -689,11 +763,15 @@ hipError_t launch_gemm_cfg(const GemmArgs& a_in, hipStream_t s) {
   return hipGetLastError();
 }
 
-// Tile shape per launch: 64 x 192 for 2-limb residual GEMMs with N = 576, 64 x 256 for the wide
-// 2-limb GEMMs (q/k/v, gate/up, the head: N >= 768, at most 1/16 of a tile column idle at N = 960),
-// 128 x 128 (64 x 128 for 4 limbs) otherwise.
+// Tile shape per launch: 32 x 64 (32 x 32 without column pairs) skinny tiles for at most 32 rows, 64 x 192 for 2-limb residual
+// GEMMs with N = 576, 64 x 256 for the wide 2-limb GEMMs (q/k/v, gate/up, the head: N >= 768, at
+// most 1/16 of a tile column idle at N = 960), 128 x 128 (64 x 128 for 4 limbs) otherwise.
 template <int AW, int EPI>
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
+  if (a.M <= 32) {
+    if constexpr (EPI == EPI_SILU || EPI == EPI_SILU_I || EPI == EPI_QKV) return launch_gemm_cfg<AW, EPI, kShapeSkinny>(a, s);
+    else return launch_gemm_cfg<AW, EPI, kShapeSkinny32>(a, s);
+  }
   if constexpr (AW == 2 && EPI == EPI_RESID)
     if (a.N % 192 == 0 && a.N % 128 != 0) return launch_gemm_cfg<AW, EPI, kShapeNarrow>(a, s);
   if constexpr (AW == 2 && EPI != EPI_RESID)

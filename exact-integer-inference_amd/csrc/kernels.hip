@@ -871,43 +871,52 @@ __global__ __launch_bounds__(256) void embed_kernel(const int64_t* ids, int M, c
 }
 
 // ------------------------------------------------------------------------------ rmsnorm
-// One wave per row; lane j holds elements j, j+64, ..., j+512.  Every product is a 32 x 32 -> 64
-// bit multiply-add: the squares through the 16-bit halves of x (python/intref.py:170-172),
-// z = RS(x U, 16) with U < 2^29 and |z| <= 2^24 (|x U| <= 2^40 since |x| <= sqrt(S)), then
-// 3 z gain.  With int16 gains (the model's, python/intref.py:126-130) |3 z gain| < 2^41, so for
-// output shifts in [10, 40] the shifted value fits int32 and saturates with one clamp; other
-// shifts take the general int64 path.  WIDE: gains anywhere in int32 (the operator entry point),
-// 3 gain and the product formed in int64 (|3 z gain| < 2^58) and saturated before narrowing.
-// u_out / z_out (trace only, nullable): U per row and z per element (python/intref.py:183).
-template <int OB, bool WIDE>
+// LPR lanes per row: 16 (4 rows per wave, for many rows) or 64 (a wave per row: a quarter of the
+// serial work per lane, for the few rows of a decoding step).  Lane c of a row holds the VW = 64 /
+// LPR columns 64 k + VW c .. + VW - 1, k = 0..8, so loads are 4 VW bytes, the limb bytes of a
+// lane's VW columns leave together, and the row sums reduce inside the lane group, where every lane
+// evaluates its own row's U.  Every product is a 32 x 32 -> 64 bit multiply-add: the squares through
+// the 16-bit halves of x (python/intref.py:170-172), z = RS(x U, 16) with U < 2^29 and |z| <= 2^24
+// (|x U| <= 2^40 since |x| <= sqrt(S)), then 3 z gain.  With int16 gains (the model's,
+// python/intref.py:126-130) |3 z gain| < 2^41, so for output shifts in [10, 40] the shifted value
+// fits int32 and saturates with one clamp; other shifts take the general int64 path.  WIDE: gains
+// anywhere in int32 (the operator entry point), 3 gain and the product formed in int64
+// (|3 z gain| < 2^58) and saturated before narrowing.  u_out / z_out (trace only, nullable): U per
+// row and z per element (python/intref.py:183).
+template <int OB, bool WIDE, int LPR>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const int32_t* x, int M, const int32_t* gain,
                                                       int sh_out, int bits_out, uint8_t* planes, void* plain,
                                                       int32_t* u_out, int32_t* z_out) {
-  // 16 lanes per row, 4 rows per wave: lane c of a row holds columns 64 k + 4 c .. + 3, k = 0..8,
-  // so loads are 16 bytes, the limb bytes of 4 columns leave as one dword, the row sums reduce in
-  // 4 steps inside the 16-lane group and each lane evaluates its own row's U
-  const int row = blockIdx.x * 16 + (threadIdx.x >> 4), c = threadIdx.x & 15;
+  static_assert(LPR == 16 || LPR == 64, "16 or 64 lanes per row");
+  constexpr int VW = 64 / LPR;
+  const int row = blockIdx.x * (256 / LPR) + threadIdx.x / LPR, c = threadIdx.x % LPR;
   const int rowc = min(row, M - 1);   // rows past M compute on row M - 1 and store nothing
-  const int32_t* xr = x + (size_t)rowc * kD + 4 * c;
-  int4 v[9], g3[9];
+  const int32_t* xr = x + (size_t)rowc * kD + VW * c;
+  int32_t v[9][VW], g3[9][VW];
+  auto load = [](const int32_t* p, int32_t (&d)[VW]) __attribute__((always_inline)) {
+    if constexpr (VW == 4) {
+      const int4 t = *(const int4*)p;
+      d[0] = t.x; d[1] = t.y; d[2] = t.z; d[3] = t.w;
+    } else {
+      d[0] = *p;
+    }
+  };
   int64_t A = 0, B = 0, Cs = 0;
 #pragma unroll
   for (int k = 0; k < 9; ++k) {
-    v[k] = *(const int4*)(xr + 64 * k);
-    g3[k] = *(const int4*)(gain + 64 * k + 4 * c);
+    load(xr + 64 * k, v[k]);
+    load(gain + 64 * k + VW * c, g3[k]);
   }
 #pragma unroll
-  for (int k = 0; k < 9; ++k) {
-    const int32_t e[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+  for (int k = 0; k < 9; ++k)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int32_t hi = e[r] >> 16, lo = e[r] & 0xFFFF;
+    for (int r = 0; r < VW; ++r) {
+      const int32_t hi = v[k][r] >> 16, lo = v[k][r] & 0xFFFF;
       A += (int64_t)hi * hi; B += (int64_t)hi * lo; Cs += (int64_t)lo * lo;
+      if constexpr (!WIDE) g3[k][r] *= 3;
     }
-    if constexpr (!WIDE) { g3[k].x *= 3; g3[k].y *= 3; g3[k].z *= 3; g3[k].w *= 3; }
-  }
 #pragma unroll
-  for (int o = 8; o > 0; o >>= 1) {
+  for (int o = LPR / 2; o > 0; o >>= 1) {
     A += __shfl_xor(A, o); B += __shfl_xor(B, o); Cs += __shfl_xor(Cs, o);
   }
   const int32_t U = (int32_t)norm_U(norm_total(A, B, Cs));   // < 2^29
@@ -931,20 +940,28 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const int32_t* x, int M, c
     };
 #pragma unroll
     for (int k = 0; k < 9; ++k) {
-      const int32_t o[4] = {norm1(v[k].x, g3[k].x), norm1(v[k].y, g3[k].y), norm1(v[k].z, g3[k].z),
-                            norm1(v[k].w, g3[k].w)};
-      if (planes) {   // K-blocked planes: columns 64 k + 4 c .. + 3 of the row at k M 64 + row 64 + 4 c
-        uint8_t* pb = planes + k * m64 + (size_t)row * 64 + 4 * c;
+      int32_t o[VW];
 #pragma unroll
-        for (int l = 0; l < OB; ++l) *(uint32_t*)(pb + l * pl) = limb_word(o, l, OB);
+      for (int r = 0; r < VW; ++r) o[r] = norm1(v[k][r], g3[k][r]);
+      const size_t e = (size_t)row * kD + 64 * k + VW * c;
+      if (planes) {   // K-blocked planes: columns 64 k + VW c .. of the row at k M 64 + row 64 + VW c
+        uint8_t* pb = planes + k * m64 + (size_t)row * 64 + VW * c;
+#pragma unroll
+        for (int l = 0; l < OB; ++l) {
+          if constexpr (VW == 4) *(uint32_t*)(pb + l * pl) = limb_word(o, l, OB);
+          else pb[l * pl] = (uint8_t)limb_byte(o[0], l, OB);
+        }
       }
       if (plain) {
-        const size_t e = (size_t)row * kD + 64 * k + 4 * c;
-        if constexpr (OB == 2) *(uint2*)((int16_t*)plain + e) = make_uint2(pack16(o[0], o[1]), pack16(o[2], o[3]));
-        else *(int4*)((int32_t*)plain + e) = make_int4(o[0], o[1], o[2], o[3]);
+        if constexpr (VW == 4 && OB == 2) *(uint2*)((int16_t*)plain + e) = make_uint2(pack16(o[0], o[1]), pack16(o[2], o[3]));
+        else if constexpr (VW == 4) *(int4*)((int32_t*)plain + e) = make_int4(o[0], o[1], o[2], o[3]);
+        else if constexpr (OB == 2) ((int16_t*)plain)[e] = (int16_t)o[0];
+        else ((int32_t*)plain)[e] = o[0];
       }
-      if (z_out)
-        *(int4*)(z_out + (size_t)row * kD + 64 * k + 4 * c) = make_int4(zof(v[k].x), zof(v[k].y), zof(v[k].z), zof(v[k].w));
+      if (z_out) {
+        if constexpr (VW == 4) *(int4*)(z_out + e) = make_int4(zof(v[k][0]), zof(v[k][1]), zof(v[k][2]), zof(v[k][3]));
+        else z_out[e] = zof(v[k][0]);
+      }
     }
   };
   if (!WIDE && sh_out >= 10 && sh_out <= 40) body(std::true_type{});
@@ -1583,17 +1600,20 @@ hipError_t embed(const int64_t* ids, int M, const int8_t* emb_q, const int32_t* 
 
 hipError_t rmsnorm(const int32_t* x, int M, const int32_t* gain, int sh_out, int bits_out, uint8_t* planes,
                    void* plain, hipStream_t s, bool wide_gain, int32_t* u_out, int32_t* z_out) {
-  dim3 grid((M + 15) / 16);
   if (bits_out != 16 && bits_out != 32) return hipErrorInvalidValue;
-#define EII_NORM(OB, W) hipLaunchKernelGGL((rmsnorm_kernel<OB, W>), grid, dim3(256), 0, s, x, M, gain, sh_out, bits_out, \
-                                           planes, plain, u_out, z_out)
+  // a wave per row while the rows leave most CUs idle anyway (shorter serial work per lane), else
+  // 16 lanes per row
+#define EII_NORM(OB, W, L) hipLaunchKernelGGL((rmsnorm_kernel<OB, W, L>), dim3((M + 256 / L - 1) / (256 / L)), dim3(256), \
+                                              0, s, x, M, gain, sh_out, bits_out, planes, plain, u_out, z_out)
+#define EII_NORM_L(OB, W) do { if (M <= 256) EII_NORM(OB, W, 64); else EII_NORM(OB, W, 16); } while (0)
   if (wide_gain) {
-    if (bits_out == 16) EII_NORM(2, true);
-    else EII_NORM(4, true);
+    if (bits_out == 16) EII_NORM_L(2, true);
+    else EII_NORM_L(4, true);
   } else {
-    if (bits_out == 16) EII_NORM(2, false);
-    else EII_NORM(4, false);
+    if (bits_out == 16) EII_NORM_L(2, false);
+    else EII_NORM_L(4, false);
   }
+#undef EII_NORM_L
 #undef EII_NORM
   return hipGetLastError();
 }

@@ -359,23 +359,20 @@ def main():
     eng.check()
     torch.cuda.synchronize()
 
-    # per-launch HIP events on the launch stream (plain launches): over the timed steps, or, when the
-    # timed steps replay graphs, over as many steps again right after them
+    # the timed steps run bare; per-launch HIP events on the launch stream (plain launches, the
+    # events between them) then time as many steps again right after them
     launches_per_step = 1 + NL * 9 + 2
     ms = (C.c_double * len(L.KERNEL_KINDS))()
     cnt = (C.c_int * len(L.KERNEL_KINDS))()
-    if not graphs:
-        L.check(lib.eii_profile_begin(eng.h, launches_per_step * args.steps + 16))
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
         step()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    if graphs:
-        L.check(lib.eii_profile_begin(eng.h, launches_per_step * args.steps + 16))
-        for _ in range(args.steps):
-            step()
+    L.check(lib.eii_profile_begin(eng.h, launches_per_step * args.steps + 16))
+    for _ in range(args.steps):
+        step()
     L.check(lib.eii_profile_end(eng.h, stream, ms, cnt))
     eng.check()
     per_kind = {k: {"ms_total": ms[i], "launches": cnt[i]} for i, k in enumerate(L.KERNEL_KINDS)}
@@ -463,9 +460,8 @@ def main():
         "forward_mfma_frac_limb_weighted": fwd_mfma_ops / (elapsed / args.steps) / PEAK_INT8_OPS,
         "kernels_ms_per_step": {k: v["ms_total"] / args.steps for k, v in per_kind.items()},
         "hip_graphs": graphs,
-        "kernels_timing": ("per-launch HIP events over the timed steps" if not graphs else
-                           "per-launch HIP events over an equal number of plain-launch steps after the timed "
-                           "graph replays"),
+        "kernels_timing": "per-launch HIP events over an equal number of plain-launch steps after the timed "
+                          "steps (which run without events)",
         "cpu_baseline": cpu,
     }
     print(json.dumps(res))

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "index_maps.h"
+
 namespace eii {
 
 enum Epi : int {
@@ -24,19 +26,8 @@ enum Epi : int {
 };
 
 // Activations enter the GEMM as int8 limb planes (eii_int.h split_limbs): a_bytes planes of
-// M x K bytes, plane l at A + l * a_plane, lowest byte first, each plane K-blocked: element
-// (m, k) at byte plane_offset(m, k, M), i.e. [K / 64][M][64], so the 64-byte K slices of
-// consecutive rows are contiguous.
-__host__ __device__ inline size_t plane_offset(size_t m, size_t k, size_t M) {
-  return (k >> 6) * M * 64 + m * 64 + (k & 63);
-}
-// The gated MLP activations (the SiLU-gate product, input of the down projection) use 32-byte K
-// blocks instead, [K / 32][M][32]: the gate/up epilogue then writes 4 consecutive rows x 32 gated
-// columns of a wave as one whole 128-byte line (no partially written lines, whose write-back
-// costs a fill from memory).  K block b of 64 bytes still starts at byte b M 64.
-__host__ __device__ inline size_t plane_offset32(size_t m, size_t k, size_t M) {
-  return (k >> 5) * M * 32 + m * 32 + (k & 31);
-}
+// M x K bytes, plane l at A + l * a_plane, lowest byte first, each plane K-blocked
+// (index_maps.h: plane_offset, or plane_offset32 for the gated MLP activations).
 // Weights enter the GEMM in MFMA fragment order (swizzle_weights): for each block of 32 output
 // rows and each 32-column K slice, the 64 lanes' 16-byte operands in lane order,
 // [ceil(N / 32)][K / 32][64][16] (lane 32 h + c: row 32 b + c, columns 16 h .. 16 h + 15 of

@@ -20,16 +20,13 @@ namespace eii {
 
 namespace {
 
+using namespace idx;   // operand layouts, fragment addresses and tile shapes (index_maps.h)
+
 constexpr int kBK = 64;          // K block: one MFMA K-step
-// LDS rows of the activation tile are 64 bytes (one K block); the 16-byte chunk c of row r sits at
-// chunk c ^ ((r >> 2) & 3), so both the direct-to-LDS loads (lane order) and the 16-lane groups of
-// the fragment reads (16 consecutive rows, one chunk) cover all 64 banks.
-constexpr int kLdsRow = 64;
 // 16 bytes per lane from global memory straight into LDS: lane i writes lds + 16 i (lds is the
 // wave's base address; every lane passes the same one).  Kept out of the kernel templates: the
 // host compilation pass of a kernel that names the builtin directly drops the kernel's launch stub.
 __device__ __forceinline__ void dma16(const void* src, void* lds) { __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 0); }
-__device__ __forceinline__ int lds_swz(int row, int c) { return c ^ ((row >> 2) & 3); }
 // s_waitcnt immediate: vector memory count <= n, the other counters not waited for (gfx9 encoding)
 constexpr int vmcnt_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
 
@@ -91,39 +88,7 @@ __device__ __forceinline__ v16i mfma32(v4i a, v4i b, v16i c) {
 // D[m][n] = sum_k a[m,k] W[n,k].  Lane = 32 h + c, register j = 4 b + r holds row
 // i = 8 b + 4 h + r, column c of the 32x32 tile: the 32 lanes of a half-wave hold 32
 // consecutive columns of one row, so every epilogue store is a contiguous run.
-// Tile shapes (4 waves, each 32 TM rows x 32 TN columns):
-//   kShapeSquare: 2 x 2 waves, 128 x 128 tiles for 2-limb activations, 64 x 128 for 4-limb;
-//   kShapeNarrow: 2 x 2 waves, 64 x 192 tiles for N a multiple of 192 but not of 128 (N = 576: three
-//     column blocks instead of four and a half, so the persistent workgroups get evenly sized tiles and
-//     no half-empty ones), 2-limb activations only;
-//   kShapeRow: 1 x 4 waves, 64 x 256 tiles for wide 2-limb GEMMs (q/k/v, gate/up, the head): the four
-//     waves share one 64-row activation tile in LDS (half the LDS traffic of a 128-row tile per MFMA
-//     column) and each loads its own weight columns;
-//   kShapeSkinny: at most 32 rows (decoding steps): one 32 x 64 tile per workgroup, the K slices split
-//     over the 4 waves, every operand fragment loaded straight into registers at the start (one memory
-//     round trip instead of a pipelined K loop whose steps each wait for a weight load), the partial
-//     sums added through LDS, and wave 0 running the epilogue; many small tiles spread the weight
-//     reads over the CUs;
-//   kShapeSkinny32: the same with 32 x 32 tiles, for the epilogues without column pairs (twice the
-//     workgroups for the narrow residual GEMMs, N = 576).
-constexpr int kShapeSquare = 0, kShapeNarrow = 1, kShapeRow = 2, kShapeSkinny = 3, kShapeSkinny32 = 4;
-template <int AW, int SHAPE = kShapeSquare>
-struct GemmCfg {
-  static constexpr bool kSkinny = SHAPE == kShapeSkinny || SHAPE == kShapeSkinny32;
-  static_assert(SHAPE == kShapeSquare || kSkinny || AW == 2, "narrow and row tiles for 2-limb activations");
-  static constexpr int kThreads = 256;                   // 4 waves; two workgroups share a CU
-  static constexpr int WGM = SHAPE == kShapeRow || kSkinny ? 1 : 2, WGN = kSkinny ? 1 : 4 / WGM;   // wave grid
-  static constexpr int BM = kSkinny ? 32 : SHAPE == kShapeSquare && AW == 2 ? 128 : 64;
-  static constexpr int BN = SHAPE == kShapeSkinny32 ? 32 : kSkinny ? 64 : SHAPE == kShapeNarrow ? 192 : SHAPE == kShapeRow ? 256 : 128;
-  static constexpr int WM = BM / WGM, WN = BN / WGN;     // wave tile
-  static constexpr int TM = WM / 32, TN = WN / 32;       // 32x32 tiles per wave
-  static constexpr int kPlane = BM * kLdsRow;
-  // activation limb planes (8 or 16 KB per stage), or for kShapeSkinny the partial sums of waves 1..3
-  static constexpr int kStage = kSkinny ? 3 * TN * AW * 16 * 64 * 4 : AW * kPlane;
-  static constexpr int kStages = kSkinny ? 1 : 4;          // loaded two and three steps ahead
-  static constexpr int kAChunks = AW * BM * 4 / kThreads;   // 16-byte direct-to-LDS loads per thread
-  static_assert(kAChunks * kThreads == AW * BM * 4, "chunk split");
-};
+// Tile shapes: GemmCfg (index_maps.h).
 
 // Tiles in grouped order: G row blocks x all column blocks per group.  Each XCD (= blockIdx % 8,
 // the hardware's round-robin dispatch) owns a contiguous range of that order, and the persistent
@@ -205,13 +170,11 @@ __global__ __launch_bounds__(256, SHAPE == kShapeSkinny || SHAPE == kShapeSkinny
     const int m0 = mb * C::BM;
 #pragma unroll
     for (int i = 0; i < C::kAChunks; ++i) {
-      // LDS slot q (16 bytes) of the stage: limb plane l, row, physical chunk cp
-      const int q = tid + C::kThreads * i, l = q / (4 * C::BM), row = (q >> 2) % C::BM, cp = q & 3;
-      const int m = min(m0 + row, g.M - 1), c = lds_swz(row, cp);
-      // 16-byte chunk c of the K block: bytes 16 c of a 64-byte row (a_kb 64), or bytes 16 (c & 1)
-      // of the row in 32-byte block c >> 1 (a_kb 32)
-      const int cb = g.a_kb >> 4;   // chunks per row of a block: 4 or 2
-      a_src[i] = Ab + (size_t)l * g.a_plane + (size_t)(c / cb) * g.M * g.a_kb + (uint32_t)(m * g.a_kb + (c % cb) * 16);
+      // LDS slot q (16 bytes) of the stage: limb plane l, row, physical chunk cp, which holds the
+      // row's logical chunk lds_swz(row, cp)
+      const AChunk ch = a_chunk(tid + C::kThreads * i, C::BM);
+      const int m = min(m0 + ch.row, g.M - 1);
+      a_src[i] = Ab + a_src_off(ch.l, m, 0, lds_swz(ch.row, ch.cp), g.M, g.a_kb, g.a_plane);
     }
   };
   auto point_w = [&](int nb) __attribute__((always_inline)) {
@@ -220,7 +183,7 @@ __global__ __launch_bounds__(256, SHAPE == kShapeSkinny || SHAPE == kShapeSkinny
       // this lane's B fragments: weight rows n0 + 64 wn + 32 tn + 0..31, the lane's 16 bytes of
       // each 32-column K slice
       const int nb32 = min((nb * C::BN + wn * C::WN + 32 * tn) >> 5, nb32_last);
-      w_src[tn] = g.W + (size_t)nb32 * ((g.w_ld ? g.w_ld : g.K) / 32) * 1024 + lane * 16;
+      w_src[tn] = g.W + w_frag(nb32, (g.w_ld ? g.w_ld : g.K) / 32, 0, lane);
     }
   };
   // The pointers advance by one K block per load.  The increment goes through an empty asm so
@@ -288,7 +251,7 @@ __global__ __launch_bounds__(256, SHAPE == kShapeSkinny || SHAPE == kShapeSkinny
     constexpr bool full = decltype(FULL)::value;
     const int m0 = mb * C::BM, n0 = nb * C::BN;
     const int rw = wm * C::WM + 4 * fh, cw = wn * C::WN + fc;
-    auto roff = [](int e) { return 8 * (e >> 2) + (e & 3); };
+    auto roff = [](int e) { return mfma_row(e, 0); };   // + 4 fh, in rw
     auto live = [&](int tm, int e) { return full || m0 + rw + 32 * tm + roff(e) < g.M; };
     const int rlast = g.M - 1 - m0;   // last valid tile row
     // the row stride passes through an empty asm so the per-element offsets are recomputed here
@@ -582,22 +545,22 @@ __global__ __launch_bounds__(256, SHAPE == kShapeSkinny || SHAPE == kShapeSkinny
     const int mb = v0 / nNB, nb = v0 % nNB;
     constexpr int NS = 2 * NK, NSW = (NS + 3) / 4;
     const int s0 = wave * NS / 4, cnt = (wave + 1) * NS / 4 - s0;
-    const int m = min(mb * C::BM + fc, g.M - 1), cb = g.a_kb >> 4;
-    const size_t wstride = (size_t)((g.w_ld ? g.w_ld : g.K) / 32) * 1024;
+    const int m = min(mb * C::BM + fc, g.M - 1);
+    const int kslices = (g.w_ld ? g.w_ld : g.K) / 32;
     // fragments as in the LDS path: row fc, bytes 16 fh .. 16 fh + 15 of slice s (chunk c of its
     // 64-byte K block in either plane layout); the weights of columns nb 64 + 32 tn + 0..31
     v4i af[NSW][AW], wf[NSW][C::TN];
 #pragma unroll
     for (int i = 0; i < NSW; ++i)
       if (i < cnt) {
-        const int sl = s0 + i, c = 2 * (sl & 1) + fh;
-        const size_t aoff = (size_t)(sl >> 1) * g.M * 64 + (size_t)(c / cb) * g.M * g.a_kb + (uint32_t)(m * g.a_kb + (c % cb) * 16);
+        const int sl = s0 + i;
+        const size_t aoff = a_src_off(0, m, sl >> 1, 2 * (sl & 1) + fh, g.M, g.a_kb, 0);
 #pragma unroll
         for (int l = 0; l < AW; ++l) af[i][l] = *(const v4i*)(Ab + (size_t)l * g.a_plane + aoff);
 #pragma unroll
         for (int tn = 0; tn < C::TN; ++tn) {
           const int nb32 = min(nb * C::TN + tn, nb32_last);
-          wf[i][tn] = *(const v4i*)(g.W + (size_t)nb32 * wstride + (size_t)sl * 1024 + lane * 16);
+          wf[i][tn] = *(const v4i*)(g.W + w_frag(nb32, kslices, sl, lane));
         }
       }
 #pragma unroll
@@ -669,7 +632,7 @@ __global__ __launch_bounds__(256, SHAPE == kShapeSkinny || SHAPE == kShapeSkinny
 #pragma unroll
         for (int l = 0; l < AW; ++l) {
           const int row = wm * C::WM + tm * 32 + fc;
-          af[tm][l] = *(const v4i*)(base + l * C::kPlane + row * kLdsRow + lds_swz(row, kc) * 16);
+          af[tm][l] = *(const v4i*)(base + a_frag(l, row, kc, C::kPlane));
         }
 #pragma unroll
       for (int tm = 0; tm < C::TM; ++tm)
@@ -819,7 +782,7 @@ __global__ __launch_bounds__(256) void swizzle_kernel(const int8_t* W, int N, in
       v = make_uint4(w[0], w[1], w[2], w[3]);
     }
   }
-  *(uint4*)(Wf + i * 16) = v;
+  *(uint4*)(Wf + w_frag((int)nb, (int)ks, (int)kc, lane)) = v;   // = Wf + 16 i
 }
 
 // out = SAT(RS(acc * mult[n], shift[n]), out_bits): thread = one element
@@ -1053,7 +1016,7 @@ __global__ __launch_bounds__(192) __attribute__((amdgpu_waves_per_eu(2))) void a
   const int hh = 3 * kvg + w;
   const int q0 = s0 + 32 * qt, qlast = min(q0 + 31, s0 + T - 1), qi = q0 + c;
   const int g0 = s0 >> 5, ntile = (qlast >> 5) - g0 + 1;
-  const int pic = 16 * ((c >> 2) & 1) + 4 * (c >> 3) + (c & 3);
+  const int pic = attn_key_perm(c);
   const int sh = a.shift_s;
   const int vts = vt_stride_for(a.M);
 

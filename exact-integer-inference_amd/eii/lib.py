@@ -93,7 +93,7 @@ def check(rc):
 
 
 def load_hostcheck():
-    """Host build of the kernels' integer helpers (eii_int.h), for CPU tests."""
+    """Host build of the kernels' integer helpers (eii_int.h) and index maps (index_maps.h), for CPU tests."""
     lib = C.CDLL(HOSTCHECK_PATH)
     for n in ("eii_host_rs", "eii_host_sat", "eii_host_norm_U", "eii_host_attn_prob",
               "eii_host_div_floor_q20"):
@@ -105,4 +105,11 @@ def load_hostcheck():
     lib.eii_host_div_floor_q20.argtypes = [C.c_int64, C.c_int64]
     lib.eii_host_limb_dot.restype = C.c_int64
     lib.eii_host_limb_dot.argtypes = [vp, vp, i32, i32]
+    # CPU model of the kernels' index maps (index_maps.h)
+    lib.eii_host_gemm_model.restype = C.c_int64
+    lib.eii_host_gemm_model.argtypes = [i32, i32, i32, i32, i32, i32, C.c_uint64, i32, vp]
+    lib.eii_host_attn_model.restype = C.c_int64
+    lib.eii_host_attn_model.argtypes = [C.c_uint64, i32]
+    lib.eii_host_wfrag_model.restype = C.c_int64
+    lib.eii_host_wfrag_model.argtypes = [i32, i32]
     return lib

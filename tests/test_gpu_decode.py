@@ -8,7 +8,9 @@ greedy generation from the 128-token prompt (exact-integer-inference.tex:167).  
   full 160-token forward (which carry the reference C checker's ALL STATES EXACT verdict);
 * appends in uneven chunks equal a full forward row for row;
 * greedy generation with the cache follows the same trajectory as greedy generation by full
-  forwards over the growing prefix.
+  forwards over the growing prefix;
+* past the 160 positions the goldens cover, single-token steps at cache lengths 225..260 equal the
+  numpy oracle's logits of the whole 260-token sequence.
 """
 import hashlib
 import json
@@ -115,6 +117,26 @@ def test_long_context_single_steps_equal_full_forward():
         del full
         e.close()
         torch.cuda.empty_cache()
+
+
+def test_steps_past_160_positions_match_oracle(eng):
+    # a 224-token prompt (tiled attention), then 36 single-token steps (the one-query decoding
+    # kernel over 225..260 cached positions), each step's logits against the oracle's row
+    from oracle.intref_np import OracleModel
+    T, P = 260, 224
+    ids_np = np.random.default_rng(260).integers(0, 49152, size=(1, T), dtype=np.int64)
+    print("oracle forward over 260 positions (about 20 s of CPU)", flush=True)
+    want = OracleModel(synth.ensure_model("base"), rope_rows=T).forward(ids_np)[2][0]
+    ids = torch.from_numpy(ids_np).to(eng.device)
+    kv = eng.kv_cache(1, T)
+    try:
+        lg = kv.append(ids[:, :P])
+        assert np.array_equal(lg[0].cpu().numpy(), want[:P])
+        for t in range(P, T):
+            lg = kv.append(ids[:, t:t + 1])
+            assert np.array_equal(lg[0, 0].cpu().numpy(), want[t]), t
+    finally:
+        kv.close()
 
 
 def test_greedy_trajectory_cached_equals_recomputed(eng):

@@ -201,6 +201,36 @@ def copy_calibration():
     print(json.dumps({"copy_calibration_bytes": COPY_BYTES, "launches": 3}))
 
 
+def vendor_gemm(steps):
+    """The vendor int8 GEMM (torch._int_mm: hipBLASLt, int8 x int8 -> int32, one pass, no epilogue) on
+    the forward's projection shapes at 256 x 160 tokens, for comparison with the limb-plane GEMMs,
+    which run 2 or 4 such passes per launch plus their fused epilogues."""
+    import torch
+    M = 40960
+    rows = []
+    for name, K, N in (("q/k/v", 576, 960), ("o", 576, 576), ("gate/up", 576, 3072), ("down", 1536, 576),
+                       ("head", 576, 49152)):
+        a = torch.randint(-128, 128, (M, K), dtype=torch.int8, device="cuda")
+        for layout in ("row-major", "column-major"):
+            w = torch.randint(-128, 128, (N, K), dtype=torch.int8, device="cuda")
+            b = w.t().contiguous() if layout == "row-major" else w.t()   # K x N operand
+            torch._int_mm(a, b)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(steps):
+                torch._int_mm(a, b)
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / steps
+            ops = 2.0 * M * N * K
+            rows.append({"gemm": name, "M": M, "K": K, "N": N, "weights": layout, "us": us,
+                         "TOP/s": ops / us * 1e-6, "of_int8_peak": ops / us * 1e-6 / (PEAK_INT8_OPS * 1e-12)})
+            del w, b
+        del a
+    print(json.dumps({"vendor_int8_gemm": "torch._int_mm (hipBLASLt)", "steps": steps, "shapes": rows}))
+
+
 def cpu_baseline_port(model_path, ids):
     sys.path.insert(0, ROOT)
     from oracle.intref_np import OracleModel
@@ -304,6 +334,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="cfg4")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--vendor-gemm", action="store_true",
+                    help="time the vendor int8 GEMM (torch._int_mm) on the forward's projection shapes")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy (the byte-counter calibration) and exit")
     ap.add_argument("--decode", action="store_true",
@@ -318,6 +350,9 @@ def main():
         return
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.vendor_gemm:
+        vendor_gemm(args.steps)
         return
     if args.decode:
         decode_bench(args)

@@ -972,8 +972,11 @@ __global__ __launch_bounds__(256) void silu_kernel(const int16_t* gu, int M, con
 }
 
 // ------------------------------------------------------------------------------ attention
-// Workgroup = the 3 query heads of one kv group for 32 queries of one sequence (wave w = head
-// 3 kvg + w); the workgroups of the longest query tiles are dispatched first.
+// Workgroup = WPG waves: query heads 3 kvg + w of kv group kvg for 32 queries of one sequence, the
+// 3 heads of the group (NKT > 0) or one (NKT == 0: the long rows, where single-wave groups let every
+// SIMD hold two waves, while 3-wave groups leave a CU two groups, 6 waves, two SIMDs with one; for
+// short rows the per-group exp table copy costs more than that gains); the waves share nothing but
+// the exp table.  The workgroups of the longest query tiles are dispatched first.
 //
 // Scores run on v_mfma_i32_32x32x32_i8 as S^T[key][query] = K . Q^T over the head dimension (two
 // K-steps of 32) with q = 256 QH + (QL' + 128), QL' = low byte - 128, QH = signed high byte, and
@@ -1001,16 +1004,21 @@ __device__ __forceinline__ int32_t sum16x8(u32x4 d, int32_t s = 0) {   // s + th
   return s;
 }
 
+constexpr int attn_wpg(int NKT) { return NKT == 0 ? 1 : 3; }
 template <int OB, int NKT>
-__global__ __launch_bounds__(192) __attribute__((amdgpu_waves_per_eu(2))) void attn_kernel(AttnArgs a) {
-  __shared__ int32_t etab[kDMax + 2];                        // exp table, etab[1537] = 0
-  __shared__ __attribute__((aligned(16))) int32_t skl[3][32];   // per wave: 128 * sum_d k per key
+__global__ __launch_bounds__(64 * attn_wpg(NKT)) __attribute__((amdgpu_waves_per_eu(2))) void attn_kernel(AttnArgs a) {
+  constexpr int WPG = attn_wpg(NKT);
+  __shared__ int32_t etab[kDMax + 2];                             // exp table, etab[1537] = 0
+  __shared__ __attribute__((aligned(16))) int32_t sklw[WPG][32];   // per wave: 128 * sum_d k per key
 
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, c = lane & 31, h = lane >> 5;
-  const int seq = blockIdx.x, kvg = blockIdx.y, qt = (a.q_first >> 5) + gridDim.z - 1 - blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, c = lane & 31, h = lane >> 5;
+  const int seq = blockIdx.x, kvg = WPG == 1 ? blockIdx.y / 3 : blockIdx.y;
+  const int w = WPG == 1 ? blockIdx.y % 3 : tid >> 6;
+  int32_t* const skl = sklw[WPG == 1 ? 0 : w];
+  const int qt = (a.q_first >> 5) + gridDim.z - 1 - blockIdx.z;
   const int s0 = a.seq_off[seq], T = a.kv_len ? a.kv_len : a.seq_off[seq + 1] - s0;
   if (32 * qt >= T) return;
-  for (int i = tid; i < kDMax + 2; i += 192) etab[i] = i <= kDMax ? a.exp_tab[i] : 0;
+  for (int i = tid; i < kDMax + 2; i += 64 * WPG) etab[i] = i <= kDMax ? a.exp_tab[i] : 0;
   __syncthreads();
 
   const int hh = 3 * kvg + w;
@@ -1066,7 +1074,7 @@ __global__ __launch_bounds__(192) __attribute__((amdgpu_waves_per_eu(2))) void a
       ks = sum16x8(d1, sum16x8(d0, ks));
     }
     ks += __shfl_xor(ks, 32);
-    skl[w][pic] = 128 * ks;   // lanes c and c + 32 store the same value
+    skl[pic] = 128 * ks;   // lanes c and c + 32 store the same value
     __builtin_amdgcn_wave_barrier();
     v16i a16 = v16i{}, a8 = v16i{}, a0 = v16i{};
 #pragma unroll
@@ -1076,7 +1084,7 @@ __global__ __launch_bounds__(192) __attribute__((amdgpu_waves_per_eu(2))) void a
       a8 = mfma32(kl[s], qh[s], a8);
       a0 = mfma32(kl[s], ql[s], a0);
     }
-    const v4i* kk = (const v4i*)&skl[w][16 * h];
+    const v4i* kk = (const v4i*)&skl[16 * h];
     const v4i k4[4] = {kk[0], kk[1], kk[2], kk[3]};
     __builtin_amdgcn_wave_barrier();
     int32_t lo[16], wv[16];
@@ -1698,7 +1706,9 @@ hipError_t attention(const AttnArgs& a, hipStream_t s) {
                    a.out_M != a.B * (a.kv_len - a.q_first)))
     return hipErrorInvalidValue;
   // query tiles from the one holding q_first (0 for a plain forward) to the end
-  const dim3 grid(a.B, kNKV, (a.max_T + 31) / 32 - (a.q_first >> 5)), block(192);
+  // (B, kv groups or heads, query tiles) workgroups of attn_wpg waves
+  const int nqt = (a.max_T + 31) / 32 - (a.q_first >> 5);
+  const dim3 grid(a.B, kNKV, nqt), block(192), grid1(a.B, kNH, nqt), block1(64);
   // up to 8 key tiles (256 keys) the scores stay in registers; beyond, every pass recomputes them
   if (a.kv_len && a.kv_len - a.q_first == 1 && a.kv_len <= kDecodeMaxKeys && a.out_M == a.B) {
     // decoding step: one query per sequence
@@ -1722,8 +1732,8 @@ hipError_t attention(const AttnArgs& a, hipStream_t s) {
     if (a.bits_c == 16) hipLaunchKernelGGL((attn_kernel<2, 8>), grid, block, 0, s, a);
     else hipLaunchKernelGGL((attn_kernel<4, 8>), grid, block, 0, s, a);
   } else {
-    if (a.bits_c == 16) hipLaunchKernelGGL((attn_kernel<2, 0>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((attn_kernel<4, 0>), grid, block, 0, s, a);
+    if (a.bits_c == 16) hipLaunchKernelGGL((attn_kernel<2, 0>), grid1, block1, 0, s, a);
+    else hipLaunchKernelGGL((attn_kernel<4, 0>), grid1, block1, 0, s, a);
   }
   return hipGetLastError();
 }

@@ -726,12 +726,15 @@ hipError_t launch_gemm_cfg(const GemmArgs& a_in, hipStream_t s) {
   return hipGetLastError();
 }
 
-// Tile shape per launch: 32 x 64 (32 x 32 without column pairs) skinny tiles for at most 32 rows, 64 x 192 for 2-limb residual
+// Tile shape per launch: 32 x 64 (32 x 32 without column pairs) skinny tiles for at most 256 rows, 64 x 192 for 2-limb residual
 // GEMMs with N = 576, 64 x 256 for the wide 2-limb GEMMs (q/k/v, gate/up, the head: N >= 768, at
 // most 1/16 of a tile column idle at N = 960), 128 x 128 (64 x 128 for 4 limbs) otherwise.
 template <int AW, int EPI>
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
-  if (a.M <= 32) {
+  // skinny tiles up to 256 rows (a 128-token prompt: 2.42 -> 1.62 ms per forward; 256 sequences'
+  // decoding step: 3.08 -> 2.08 ms), except for the head beyond 32 rows, whose 28 MB of weights each
+  // 32-row block would read again (the 64-row tiles read them half as often)
+  if (a.M <= 256 && (EPI != EPI_LOGITS || a.M <= 32)) {
     if constexpr (EPI == EPI_SILU || EPI == EPI_SILU_I || EPI == EPI_QKV) return launch_gemm_cfg<AW, EPI, kShapeSkinny>(a, s);
     else return launch_gemm_cfg<AW, EPI, kShapeSkinny32>(a, s);
   }
@@ -973,10 +976,11 @@ __global__ __launch_bounds__(256) void silu_kernel(const int16_t* gu, int M, con
 
 // ------------------------------------------------------------------------------ attention
 // Workgroup = WPG waves: query heads 3 kvg + w of kv group kvg for 32 queries of one sequence, the
-// 3 heads of the group (NKT > 0) or one (NKT == 0: the long rows, where single-wave groups let every
-// SIMD hold two waves, while 3-wave groups leave a CU two groups, 6 waves, two SIMDs with one; for
-// short rows the per-group exp table copy costs more than that gains); the waves share nothing but
-// the exp table.  The workgroups of the longest query tiles are dispatched first.
+// 3 heads of the group (up to 8 key tiles) or one (the long rows: single-wave groups let every SIMD
+// hold two waves where 3-wave groups leave a CU two groups, 6 waves, two SIMDs with one; for short
+// rows the per-group exp table copy costs more than that gains, at 256 sequences and at one).  The
+// waves share nothing but the exp table.  The workgroups of the longest query tiles are dispatched
+// first.
 //
 // Scores run on v_mfma_i32_32x32x32_i8 as S^T[key][query] = K . Q^T over the head dimension (two
 // K-steps of 32) with q = 256 QH + (QL' + 128), QL' = low byte - 128, QH = signed high byte, and
@@ -1004,10 +1008,9 @@ __device__ __forceinline__ int32_t sum16x8(u32x4 d, int32_t s = 0) {   // s + th
   return s;
 }
 
-constexpr int attn_wpg(int NKT) { return NKT == 0 ? 1 : 3; }
-template <int OB, int NKT>
-__global__ __launch_bounds__(64 * attn_wpg(NKT)) __attribute__((amdgpu_waves_per_eu(2))) void attn_kernel(AttnArgs a) {
-  constexpr int WPG = attn_wpg(NKT);
+template <int OB, int NKT, int WPG>
+__global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) void attn_kernel(AttnArgs a) {
+  static_assert(WPG == 1 || WPG == 3, "one wave per head, or the 3 heads of a kv group");
   __shared__ int32_t etab[kDMax + 2];                             // exp table, etab[1537] = 0
   __shared__ __attribute__((aligned(16))) int32_t sklw[WPG][32];   // per wave: 128 * sum_d k per key
 
@@ -1705,11 +1708,6 @@ hipError_t attention(const AttnArgs& a, hipStream_t s) {
   if (a.kv_len && (a.q_first < 0 || a.q_first >= a.kv_len || a.max_T != a.kv_len ||
                    a.out_M != a.B * (a.kv_len - a.q_first)))
     return hipErrorInvalidValue;
-  // query tiles from the one holding q_first (0 for a plain forward) to the end
-  // (B, kv groups or heads, query tiles) workgroups of attn_wpg waves
-  const int nqt = (a.max_T + 31) / 32 - (a.q_first >> 5);
-  const dim3 grid(a.B, kNKV, nqt), block(192), grid1(a.B, kNH, nqt), block1(64);
-  // up to 8 key tiles (256 keys) the scores stay in registers; beyond, every pass recomputes them
   if (a.kv_len && a.kv_len - a.q_first == 1 && a.kv_len <= kDecodeMaxKeys && a.out_M == a.B) {
     // decoding step: one query per sequence
     // 4 waves per head while the workgroups (3 per sequence) leave most CUs idle
@@ -1725,15 +1723,20 @@ hipError_t attention(const AttnArgs& a, hipStream_t s) {
     }
     return hipGetLastError();
   }
+  // query tiles from the one holding q_first (0 for a plain forward) to the end; workgroups of the
+  // 3 heads of a kv group while up to 8 key tiles (256 keys) keep their scores in registers, of one
+  // head for the longer rows, whose passes recompute the scores
+  const int nqt = (a.max_T + 31) / 32 - (a.q_first >> 5);
+  const dim3 grid(a.B, kNKV, nqt), block(192), grid1(a.B, kNH, nqt), block1(64);
   if (a.max_kt <= 5) {
-    if (a.bits_c == 16) hipLaunchKernelGGL((attn_kernel<2, 5>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((attn_kernel<4, 5>), grid, block, 0, s, a);
+    if (a.bits_c == 16) hipLaunchKernelGGL((attn_kernel<2, 5, 3>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((attn_kernel<4, 5, 3>), grid, block, 0, s, a);
   } else if (a.max_kt <= 8) {
-    if (a.bits_c == 16) hipLaunchKernelGGL((attn_kernel<2, 8>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((attn_kernel<4, 8>), grid, block, 0, s, a);
+    if (a.bits_c == 16) hipLaunchKernelGGL((attn_kernel<2, 8, 3>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((attn_kernel<4, 8, 3>), grid, block, 0, s, a);
   } else {
-    if (a.bits_c == 16) hipLaunchKernelGGL((attn_kernel<2, 0>), grid1, block1, 0, s, a);
-    else hipLaunchKernelGGL((attn_kernel<4, 0>), grid1, block1, 0, s, a);
+    if (a.bits_c == 16) hipLaunchKernelGGL((attn_kernel<2, 0, 1>), grid1, block1, 0, s, a);
+    else hipLaunchKernelGGL((attn_kernel<4, 0, 1>), grid1, block1, 0, s, a);
   }
   return hipGetLastError();
 }

@@ -220,6 +220,15 @@ def test_attention_scores_at_floor(oracle, lens):
     _attention_case(oracle, lens, scale=20000.0, seed=11 + len(lens), f_qr=8, f_kr=8, floor=True)
 
 
+@pytest.mark.parametrize("nseq,lo,hi", [(40, 130, 161), (24, 200, 251)])
+def test_attention_large_batches(oracle, nseq, lo, hi):
+    # many ragged sequences (starts off the 32-row tile grid) in one launch, up to 5 and up to 8
+    # key tiles
+    lens = list(np.random.default_rng(nseq).integers(lo, hi, size=nseq))
+    _attention_case(oracle, lens, scale=2000.0, seed=nseq)
+    _attention_case(oracle, lens, scale=20000.0, seed=nseq + 1, f_qr=8, f_kr=8, floor=True)
+
+
 def test_attention_ctx32(oracle):
     _attention_case(oracle, [100], scale=3000.0, seed=5, f_c=27, bits_c=32)
 

@@ -253,6 +253,10 @@ __global__ __launch_bounds__(256, SHAPE == kShapeSkinny || SHAPE == kShapeSkinny
     const int rw = wm * C::WM + 4 * fh, cw = wn * C::WN + fc;
     auto roff = [](int e) { return mfma_row(e, 0); };   // + 4 fh, in rw
     auto live = [&](int tm, int e) { return full || m0 + rw + 32 * tm + roff(e) < g.M; };
+    // a group of the wave's rows whose first row (tile row 32 tm + r0, lane half 0) lies past M: the
+    // SiLU and q/k/v epilogues skip the whole group, a uniform branch (the last row block of a
+    // launch; a skinny tile of a one-sequence decoding step keeps 1 of its 8 groups of 4 rows)
+    auto dead = [&](int tm, int r0) { return !full && m0 + wm * C::WM + 32 * tm + r0 >= g.M; };
     const int rlast = g.M - 1 - m0;   // last valid tile row
     // the row stride passes through an empty asm so the per-element offsets are recomputed here
     // instead of being hoisted out of the tile loop (64 loop-invariant offsets would spill)
@@ -409,6 +413,7 @@ __global__ __launch_bounds__(256, SHAPE == kShapeSkinny || SHAPE == kShapeSkinny
         for (int tm = 0; tm < C::TM; ++tm) {
 #pragma unroll
           for (int b = 0; b < 4; ++b) {   // rows 8 b + 4 h + 0..3 of the 32-row tile tm
+            if (dead(tm, 8 * b)) continue;
             int32_t gv[4], sv[4], ui[4], vv[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) { gv[r] = value16(tm, 0, 4 * b + r); ui[r] = value16(tm, 1, 4 * b + r); }
@@ -472,6 +477,7 @@ __global__ __launch_bounds__(256, SHAPE == kShapeSkinny || SHAPE == kShapeSkinny
           for (int tm = 0; tm < C::TM; ++tm) {
 #pragma unroll
             for (int b = 0; b < 4; ++b) {
+              if (dead(tm, 8 * b)) continue;
               int32_t v1[4], v2[4];
 #pragma unroll
               for (int r = 0; r < 4; ++r) {
@@ -501,6 +507,7 @@ __global__ __launch_bounds__(256, SHAPE == kShapeSkinny || SHAPE == kShapeSkinny
           for (int tm = 0; tm < C::TM; ++tm) {
 #pragma unroll
             for (int b = 0; b < 4; ++b) {
+              if (dead(tm, 8 * b)) continue;
               int32_t cs[4], sn[4];
 #pragma unroll
               for (int r = 0; r < 4; ++r) {

@@ -41,6 +41,8 @@ CASES = [
     (2, ROW, 65, 3072, 64, 64),
     (2, SKINNY, 1, 3072, 576, 64),      # decoding: gate/up
     (2, SKINNY, 17, 960, 576, 64),
+    (2, SKINNY, 200, 3072, 128, 64),   # skinny tiles serve up to 256 rows
+    (4, SKINNY32, 129, 576, 192, 32),
     (4, SKINNY32, 3, 576, 1536, 32),    # decoding: down
     (2, SKINNY32, 32, 576, 576, 64),
     (4, SKINNY, 5, 128, 192, 64),

@@ -1168,25 +1168,22 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
       return __builtin_amdgcn_perm(__builtin_amdgcn_perm(v[3], v[2], 0x0c0c0400u),
                                    __builtin_amdgcn_perm(v[1], v[0], 0x0c0c0400u), 0x05040100u);
     };
-    uint32_t w0[4], w1[4], wb[4], wc[4];
+    uint32_t w0[4], w1[4];
+    int32_t R1s[16];   // kept for the extra parts, which only waves with some R1 > 127 form
     int32_t rmax = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      int32_t P[4], p1[4], pb[4], pc[4];
+      int32_t P[4], p1[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         P[r] = prob(ev[4 * i + r]);
-        const int32_t R1 = (P[r] + 128) >> 8;
-        rmax = max(rmax, R1);
-        p1[r] = min(R1, 127);
-        pb[r] = min(R1 - p1[r], 127);
-        pc[r] = R1 - p1[r] - pb[r];
+        R1s[4 * i + r] = (P[r] + 128) >> 8;
+        rmax = max(rmax, R1s[4 * i + r]);
+        p1[r] = min(R1s[4 * i + r], 127);
       }
       SP += (P[0] + P[1]) + (P[2] + P[3]);
       w0[i] = bytes4(P);    // low bytes of P
       w1[i] = bytes4(p1);
-      wb[i] = bytes4(pb);
-      wc[i] = bytes4(pc);
     }
     const v4i P0 = v4i{(int)w0[0], (int)w0[1], (int)w0[2], (int)w0[3]};
     const v4i P1 = v4i{(int)w1[0], (int)w1[1], (int)w1[2], (int)w1[3]};
@@ -1200,6 +1197,19 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
       C0[dt] = mfma32(VL[dt], P0, C0[dt]);
     }
     if (__any(rmax > 127)) {
+      uint32_t wb[4], wc[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        int32_t pb[4], pc[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int32_t R1 = R1s[4 * i + r], p1 = min(R1, 127);
+          pb[r] = min(R1 - p1, 127);
+          pc[r] = R1 - p1 - pb[r];
+        }
+        wb[i] = bytes4(pb);
+        wc[i] = bytes4(pc);
+      }
       const v4i P1b = v4i{(int)wb[0], (int)wb[1], (int)wb[2], (int)wb[3]};
       const v4i P1c = v4i{(int)wc[0], (int)wc[1], (int)wc[2], (int)wc[3]};
       const bool three = __any(rmax > 254);

@@ -133,6 +133,8 @@ struct eii_kv {
   int device = 0;
   int B = 0, cap = 0;              // sequences, positions per sequence (a multiple of 32)
   int len = 0;                     // positions held by every sequence
+  int vt_len = 0;                  // positions whose V^T planes are written (single-token steps
+                                   // served by the one-query decoding kernel leave them out)
   uint8_t* dev = nullptr;          // one allocation for all layers
   int16_t* qkv[kNL] = {};
   uint8_t* vt[kNL] = {};
@@ -581,10 +583,12 @@ hipError_t copy_cols(void* dst, int dst_w, const void* src, int src_w, int col0,
 // context and the gated product live in m->h, m->ctx and m->gated as int8 limb planes; with a
 // trace the unfused q/k/v and gate/up projections run so their values can be dumped, and the
 // producers also write plain copies into the trace buffers.
-// One step of incremental decoding: T_new new positions of every sequence, from position p0.
+// One step of incremental decoding: T_new new positions of every sequence, from position p0;
+// vt: the step's attention reads the V^T planes (the tiled kernel), so the append writes them too.
 struct KvStep {
   eii_kv* kv;
   int T_new, p0;
+  bool vt;
 };
 
 int run_block(eii_model* m, int l, int32_t* x, int M, int nseq, int max_T, const eii_trace* tr, hipStream_t s,
@@ -605,8 +609,13 @@ int run_block(eii_model* m, int l, int32_t* x, int M, int nseq, int max_T, const
       g.pos = m->pos; g.cosT = m->rope_c; g.sinT = m->rope_s; g.sh_q = sh_q; g.sh_k = sh_k;
       if (!kv) { g.vt = m->vt; g.vt_stride = vt_stride_for(M); }
       HIPCHK(gemm(g, hb, EPI_QKV, s));
-      // decoding: the new rows join the cache, whose V^T planes take their v columns
-      if (kv) HIPCHK(kv_append(m->qkv, nseq, kv->T_new, kv->kv->cap, kv->p0, kv->kv->qkv[l], kv->kv->vt[l], s));
+      // decoding: the new rows join the cache; when this step's attention reads the V^T planes,
+      // the positions that earlier single-token steps left out get theirs first
+      if (kv) {
+        eii_kv* c = kv->kv;
+        if (kv->vt) HIPCHK(kv_build_vt(c->qkv[l], nseq, c->cap, c->vt_len, kv->p0, c->vt[l], s));
+        HIPCHK(kv_append(m->qkv, nseq, kv->T_new, c->cap, kv->p0, c->qkv[l], kv->vt ? c->vt[l] : nullptr, s));
+      }
     } else {
       HIPCHK(gemm(g, hb, EPI_REQ16, s));
     }
@@ -878,6 +887,7 @@ extern "C" int eii_kv_length(const eii_kv* kv) { return kv ? kv->len : 0; }
 extern "C" int eii_kv_reset(eii_kv* kv) {
   if (!kv) return fail(EII_E_ARG, "null kv cache");
   kv->len = 0;
+  kv->vt_len = 0;
   return EII_OK;
 }
 
@@ -902,10 +912,14 @@ extern "C" int eii_kv_append(eii_model* m, eii_kv* kv, const int64_t* ids, int T
     ProfScope ps(m, EII_K_EMBED, s);
     HIPCHK(embed(ids, (int)M, m->emb_q, m->emb_m, m->emb_sh, m->x, m->flags, s));
   }
-  const KvStep step{kv, T_new, p0};
+  // the one-query decoding kernel (a single new position, at most kDecodeMaxKeys cached) reads
+  // the cache rows only; every other step takes the tiled kernel, which reads the V^T planes
+  const bool vt = !(T_new == 1 && len <= kDecodeMaxKeys);
+  const KvStep step{kv, T_new, p0, vt};
   for (int l = 0; l < kNL; ++l)
     if ((rc = run_block(m, l, m->x, (int)M, kv->B, len, nullptr, s, &step))) return rc;
   kv->len = len;
+  if (vt) kv->vt_len = len;
   if (logits) return run_final(m, m->x, (int)M, logits, s);
   return EII_OK;
 }

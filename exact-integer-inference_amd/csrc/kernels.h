@@ -153,9 +153,16 @@ inline int attn_key_tiles(int s0, int T) { return ((s0 + T - 1) >> 5) - (s0 >> 5
 hipError_t attention(const AttnArgs& a, hipStream_t s);
 
 // KV cache append: rows b T_new + i of qkv [B T_new, 960] go to row b cap + p0 + i of the cache
-// rows and, for the v columns, to the cache's V^T limb planes (vt_stride_for(B cap))
+// rows and, for the v columns, to the cache's V^T limb planes (vt_stride_for(B cap)) unless
+// cache_vt is null
 hipError_t kv_append(const int16_t* qkv, int B, int T_new, int cap, int p0, int16_t* cache_qkv, uint8_t* cache_vt,
                      hipStream_t s);
+// V^T planes of the cached positions [from, to) of every sequence, rebuilt from the cached v rows
+// (single-token appends that the one-query decoding kernel serves leave them out)
+hipError_t kv_build_vt(const int16_t* cache_qkv, int B, int cap, int from, int to, uint8_t* cache_vt, hipStream_t s);
+// longest cache the one-query decoding attention serves (its scores of 3 heads sit in LDS); longer
+// caches take the tiled kernel, which reads the V^T planes
+constexpr int kDecodeMaxKeys = 8192;
 // pos[b T_new + i] = p0 + i
 hipError_t fill_positions(int32_t* pos, int B, int T_new, int p0, hipStream_t s);
 // out[r] = the lowest index of the largest of the n values of row r

@@ -1405,7 +1405,7 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
 // with each P taken from its lane by v_readlane, and the head's 4 partial sums meet in LDS.  A
 // wave's first value chunk is loaded before the reductions, so its latency hides behind them.
 // No key is masked: every cached key precedes the query.
-constexpr int kDecodeMaxKeys = 8192;   // scores of 3 heads x 8192 keys: 48 KB of LDS
+// scores of 3 heads x kDecodeMaxKeys keys: 48 KB of LDS (kernels.h)
 // LDS: exp table [1537] + 3 pad ints (the end stays 16-byte aligned), the row maxima [3 NW] in an
 // even count of ints (so the int64 arrays after them are 8-byte aligned for every NW), the exp sums
 // [3 NW] and partial context sums [3 NW][64] as int64, the scores of 3 heads as int16
@@ -1768,11 +1768,24 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const int16_t* qkv, int 
   const size_t crow = (size_t)b * cap + p0 + t;
   const int16_t v = qkv[i];
   cache[crow * kQKVN + col] = v;
-  if (col >= kD + 192) {
+  if (vt && col >= kD + 192) {
     const size_t d = col - kD - 192;
     vt[d * stride + crow] = (uint8_t)((uint32_t)v ^ 0x80u);
     vt[(size_t)192 * stride + d * stride + crow] = (uint8_t)((uint32_t)v >> 8);
   }
+}
+
+// V^T planes of cached positions [from, to) of every sequence, from the cached v rows: thread =
+// (plane, d, sequence, position), positions fastest, so each store run is contiguous
+__global__ __launch_bounds__(256) void kv_vt_kernel(const int16_t* cache, int B, int cap, int from, int to,
+                                                    uint8_t* vt, int stride) {
+  const int n = to - from;
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (size_t)2 * 192 * B * n) return;
+  const int t = (int)(i % n), b = (int)(i / n % B), d = (int)(i / ((size_t)n * B) % 192), l = (int)(i / ((size_t)n * B * 192));
+  const size_t crow = (size_t)b * cap + from + t;
+  const uint32_t v = (uint16_t)cache[crow * kQKVN + kD + 192 + d];
+  vt[(size_t)l * 192 * stride + (size_t)d * stride + crow] = (uint8_t)(l ? v >> 8 : v ^ 0x80u);
 }
 
 hipError_t kv_append(const int16_t* qkv, int B, int T_new, int cap, int p0, int16_t* cache_qkv, uint8_t* cache_vt,
@@ -1780,6 +1793,14 @@ hipError_t kv_append(const int16_t* qkv, int B, int T_new, int cap, int p0, int1
   if (B <= 0 || T_new <= 0 || p0 < 0 || p0 + T_new > cap) return hipErrorInvalidValue;
   hipLaunchKernelGGL(kv_append_kernel, dim3(blocks_for((size_t)B * T_new * kQKVN)), dim3(256), 0, s, qkv, B, T_new,
                      cap, p0, cache_qkv, cache_vt, vt_stride_for(B * cap));
+  return hipGetLastError();
+}
+
+hipError_t kv_build_vt(const int16_t* cache_qkv, int B, int cap, int from, int to, uint8_t* cache_vt, hipStream_t s) {
+  if (B <= 0 || from < 0 || to > cap || from > to) return hipErrorInvalidValue;
+  if (from == to) return hipSuccess;
+  hipLaunchKernelGGL(kv_vt_kernel, dim3(blocks_for((size_t)2 * 192 * B * (to - from))), dim3(256), 0, s, cache_qkv, B,
+                     cap, from, to, cache_vt, vt_stride_for(B * cap));
   return hipGetLastError();
 }
 

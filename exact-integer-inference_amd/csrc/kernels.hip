@@ -982,12 +982,11 @@ __global__ __launch_bounds__(256) void silu_kernel(const int16_t* gu, int M, con
 }
 
 // ------------------------------------------------------------------------------ attention
-// Workgroup = WPG waves: query heads 3 kvg + w of kv group kvg for 32 queries of one sequence, the
-// 3 heads of the group (up to 8 key tiles) or one (the long rows: single-wave groups let every SIMD
-// hold two waves where 3-wave groups leave a CU two groups, 6 waves, two SIMDs with one; for short
-// rows the per-group exp table copy costs more than that gains, at 256 sequences and at one).  The
-// waves share nothing but the exp table.  The workgroups of the longest query tiles are dispatched
-// first.
+// A wave computes one query head 3 kvg + w (kv group kvg) for 32 queries of one sequence.  Up to 8
+// key tiles a workgroup holds 4 such waves, consecutive in the order [query tile from the last]
+// [sequence][head], so two workgroups fill a CU's 4 SIMDs with two waves each and share the exp
+// table copy; the long rows run one wave per workgroup.  The waves share nothing but the exp
+// table.  The longest query tiles are dispatched first.
 //
 // Scores run on v_mfma_i32_32x32x32_i8 as S^T[key][query] = K . Q^T over the head dimension (two
 // K-steps of 32) with q = 256 QH + (QL' + 128), QL' = low byte - 128, QH = signed high byte, and
@@ -1017,19 +1016,36 @@ __device__ __forceinline__ int32_t sum16x8(u32x4 d, int32_t s = 0) {   // s + th
 
 template <int OB, int NKT, int WPG>
 __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) void attn_kernel(AttnArgs a) {
-  static_assert(WPG == 1 || WPG == 3, "one wave per head, or the 3 heads of a kv group");
+  static_assert(WPG == 1 || WPG == 4, "one wave per workgroup, or 4 independent waves");
   __shared__ int32_t etab[kDMax + 2];                             // exp table, etab[1537] = 0
   __shared__ __attribute__((aligned(16))) int32_t sklw[WPG][32];   // per wave: 128 * sum_d k per key
 
   const int tid = threadIdx.x, lane = tid & 63, c = lane & 31, h = lane >> 5;
-  const int seq = blockIdx.x, kvg = WPG == 1 ? blockIdx.y / 3 : blockIdx.y;
-  const int w = WPG == 1 ? blockIdx.y % 3 : tid >> 6;
-  int32_t* const skl = sklw[WPG == 1 ? 0 : w];
-  const int qt = (a.q_first >> 5) + gridDim.z - 1 - blockIdx.z;
+  int32_t* const skl = sklw[WPG == 1 ? 0 : tid >> 6];
+  // this wave's (sequence, query head 3 kvg + w, query tile qt)
+  int seq, kvg, w, qt;
+  bool idle = false;
+  if constexpr (WPG == 1) {
+    seq = blockIdx.x;
+    kvg = blockIdx.y / 3;
+    w = blockIdx.y % 3;
+    qt = (a.q_first >> 5) + gridDim.z - 1 - blockIdx.z;
+  } else {
+    // task = 4 blockIdx.x + wave over [query tiles from the last][sequences][heads]
+    const int nqt = (a.max_T + 31) / 32 - (a.q_first >> 5), per = a.B * kNH;
+    const int task = 4 * (int)blockIdx.x + (tid >> 6), qr = task / per, rem = task - qr * per;
+    idle = qr >= nqt;
+    seq = idle ? 0 : rem / kNH;
+    kvg = rem % kNH / 3;
+    w = rem % 3;
+    qt = (a.q_first >> 5) + nqt - 1 - qr;
+  }
   const int s0 = a.seq_off[seq], T = a.kv_len ? a.kv_len : a.seq_off[seq + 1] - s0;
-  if (32 * qt >= T) return;
+  idle = idle || 32 * qt >= T;
+  if (WPG == 1 && idle) return;
   for (int i = tid; i < kDMax + 2; i += 64 * WPG) etab[i] = i <= kDMax ? a.exp_tab[i] : 0;
   __syncthreads();
+  if (idle) return;   // (no workgroup barrier follows)
 
   const int hh = 3 * kvg + w;
   const int q0 = s0 + 32 * qt, qlast = min(q0 + 31, s0 + T - 1), qi = q0 + c;
@@ -1744,13 +1760,13 @@ hipError_t attention(const AttnArgs& a, hipStream_t s) {
   // 3 heads of a kv group while up to 8 key tiles (256 keys) keep their scores in registers, of one
   // head for the longer rows, whose passes recompute the scores
   const int nqt = (a.max_T + 31) / 32 - (a.q_first >> 5);
-  const dim3 grid(a.B, kNKV, nqt), block(192), grid1(a.B, kNH, nqt), block1(64);
+  const dim3 grid((unsigned)(((size_t)nqt * a.B * kNH + 3) / 4)), block(256), grid1(a.B, kNH, nqt), block1(64);
   if (a.max_kt <= 5) {
-    if (a.bits_c == 16) hipLaunchKernelGGL((attn_kernel<2, 5, 3>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((attn_kernel<4, 5, 3>), grid, block, 0, s, a);
+    if (a.bits_c == 16) hipLaunchKernelGGL((attn_kernel<2, 5, 4>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((attn_kernel<4, 5, 4>), grid, block, 0, s, a);
   } else if (a.max_kt <= 8) {
-    if (a.bits_c == 16) hipLaunchKernelGGL((attn_kernel<2, 8, 3>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((attn_kernel<4, 8, 3>), grid, block, 0, s, a);
+    if (a.bits_c == 16) hipLaunchKernelGGL((attn_kernel<2, 8, 4>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((attn_kernel<4, 8, 4>), grid, block, 0, s, a);
   } else {
     if (a.bits_c == 16) hipLaunchKernelGGL((attn_kernel<2, 0, 1>), grid1, block1, 0, s, a);
     else hipLaunchKernelGGL((attn_kernel<4, 0, 1>), grid1, block1, 0, s, a);

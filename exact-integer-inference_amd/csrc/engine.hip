@@ -608,10 +608,17 @@ int run_block(eii_model* m, int l, int32_t* x, int M, int nseq, int max_T, const
     if (!tr) {   // q, k, v projections with RoPE and the V^T planes in the epilogue
       g.pos = m->pos; g.cosT = m->rope_c; g.sinT = m->rope_s; g.sh_q = sh_q; g.sh_k = sh_k;
       if (!kv) { g.vt = m->vt; g.vt_stride = vt_stride_for(M); }
+      // a single-token step whose attention reads no V^T planes writes its rows straight into
+      // their cache rows (row b at position p0 of sequence b: stride cap rows)
+      const bool direct = kv && !kv->vt && kv->T_new == 1 && (int64_t)kv->kv->cap * kQKVN * 64 < ((int64_t)1 << 31);
+      if (direct) {
+        g.out = kv->kv->qkv[l] + (size_t)kv->p0 * kQKVN;
+        g.ldc = kv->kv->cap * kQKVN;
+      }
       HIPCHK(gemm(g, hb, EPI_QKV, s));
       // decoding: the new rows join the cache; when this step's attention reads the V^T planes,
       // the positions that earlier single-token steps left out get theirs first
-      if (kv) {
+      if (kv && !direct) {
         eii_kv* c = kv->kv;
         if (kv->vt) HIPCHK(kv_build_vt(c->qkv[l], nseq, c->cap, c->vt_len, kv->p0, c->vt[l], s));
         HIPCHK(kv_append(m->qkv, nseq, kv->T_new, c->cap, kv->p0, c->qkv[l], kv->vt ? c->vt[l] : nullptr, s));

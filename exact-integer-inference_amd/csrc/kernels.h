@@ -61,6 +61,9 @@ struct GemmArgs {
   // EPI_QKV: also write v as the key-contiguous V^T limb planes described below, or null
   uint8_t* vt = nullptr;
   int vt_stride = 0;
+  // EPI_QKV: elements between output rows (0 = N), so a decoding step's rows can go straight to
+  // their KV cache rows (row r at out + r ldc); 32 ldc 2 bytes must stay below 2^31
+  int ldc = 0;
   // K of the whole fragment-ordered weight matrix when this launch covers a range of its K blocks
   // (W and A then point at the first block of the range); 0 = K
   int w_ld = 0;

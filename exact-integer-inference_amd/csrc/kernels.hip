@@ -467,8 +467,10 @@ __global__ __launch_bounds__(256, SHAPE == kShapeSkinny || SHAPE == kShapeSkinny
         }
       } else {   // EPI_QKV: heads 0..8 q and 9..11 k get RoPE, 12..14 v are stored as they are
         const int head = (n0 + wn * C::WN) >> 6;
-        int16_t* tb = (int16_t*)g.out + (size_t)m0 * N + n0;
-        const uint32_t lane_b = ((uint32_t)rw * (uint32_t)N + (uint32_t)cw) * 2u;
+        int ld = g.ldc ? g.ldc : g.N;   // output row stride, opaque like N
+        __asm__ volatile("" : "+s"(ld));
+        int16_t* tb = (int16_t*)g.out + (size_t)m0 * ld + n0;
+        const uint32_t lane_b = ((uint32_t)rw * (uint32_t)ld + (uint32_t)cw) * 2u;
         if (head >= 12) {
           // v: int16 rows and, when requested, the V^T limb planes (4 consecutive rows per dword;
           // rows up to the tile end fit vt_stride, so no row test there)
@@ -485,7 +487,7 @@ __global__ __launch_bounds__(256, SHAPE == kShapeSkinny || SHAPE == kShapeSkinny
                 v1[r] = value16(tm, 0, e);
                 v2[r] = value16(tm, 1, e);
                 if (live(tm, e)) {
-                  int16_t* op = at(tb, N, lane_b, tm, e, 0);
+                  int16_t* op = at(tb, ld, lane_b, tm, e, 0);
                   op[0] = (int16_t)v1[r];
                   op[32] = (int16_t)v2[r];
                 }
@@ -524,7 +526,7 @@ __global__ __launch_bounds__(256, SHAPE == kShapeSkinny || SHAPE == kShapeSkinny
                 const int32_t o1 = rne_i32(fmin(fmax(fma(fma(a1, c, -a2 * s2), sc, half), -32768.0), 32767.0));
                 const int32_t o2 = rne_i32(fmin(fmax(fma(fma(a2, c, a1 * s2), sc, half), -32768.0), 32767.0));
                 if (!live(tm, e)) continue;
-                int16_t* op = at(tb, N, lane_b, tm, e, 0);
+                int16_t* op = at(tb, ld, lane_b, tm, e, 0);
                 op[0] = (int16_t)o1;
                 op[32] = (int16_t)o2;
               }
@@ -1568,6 +1570,7 @@ inline unsigned blocks_for(size_t n) { return (unsigned)((n + 255) / 256); }
 
 hipError_t gemm(const GemmArgs& a, int a_bytes, int epi, hipStream_t s) {
   if (a.K % kBK != 0 || a.M <= 0 || a.N <= 0 || a.N % 4 != 0) return hipErrorInvalidValue;
+  if (a.ldc && (epi != EPI_QKV || a.ldc < a.N || (int64_t)a.ldc * 64 >= ((int64_t)1 << 31))) return hipErrorInvalidValue;
   if (a_bytes == 2 && epi != EPI_I64 && !a.coef) return hipErrorInvalidValue;
 #define EII_EPIS(AW)                                                     \
   switch (epi) {                                                         \

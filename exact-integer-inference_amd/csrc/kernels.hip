@@ -1010,6 +1010,7 @@ __global__ __launch_bounds__(256) void silu_kernel(const int16_t* gu, int M, con
 // exp-sum and probability passes; NKT == 0: every pass recomputes the scores (long sequences).
 constexpr int32_t kMasked = -32768;   // no score exceeds it, so the row max never picks it
 
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ int32_t sum16x8(u32x4 d, int32_t s = 0) {   // s + the 8 int16 values in d
 #pragma unroll
   for (int i = 0; i < 4; ++i) s += ((int32_t)(d[i] << 16) >> 16) + ((int32_t)d[i] >> 16);
@@ -1130,12 +1131,19 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
       for (int j = 0; j < 16; ++j)
         sc[j] = min(max(min(max(wv[j], -32769), 32768) * (1 << (16 - sh)) + ((lo[j] & 0xFFFF) >> sh), -32768), 32767);
     }
-    if (32 * g < s0 || 32 * g + 31 > q0) {
+    // keys past the query (the diagonal tile) and before the sequence start (its first tile when
+    // the sequence does not start on a tile boundary): key 32 g + 16 h + j
+    if (32 * g + 31 > q0) {
+      const int last = qi - 32 * g - 16 * h;
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int key = 32 * g + 16 * h + j;
-        if (key < s0 || key > qi) sc[j] = kMasked;
-      }
+      for (int j = 0; j < 16; ++j)
+        if (j > last) sc[j] = kMasked;
+    }
+    if (32 * g < s0) {
+      const int first = s0 - 32 * g - 16 * h;
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        if (j < first) sc[j] = kMasked;
     }
   };
   // e = E[rowmax - s] for d <= 1536, else 0; masked keys 0
@@ -1320,21 +1328,42 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
       }
     }
     rowmax = max(rowmax, __shfl_xor(rowmax, 32));
-    auto unpack = [&](int t, int j) __attribute__((always_inline)) -> int32_t {
-      const uint32_t p = pk[t][j >> 1];
-      return (j & 1) ? (int32_t)p >> 16 : (int32_t)(p << 16) >> 16;
-    };
-    // e = E[min(rowmax - s, 1537)] directly, with no key tests: a masked key holds score kMasked,
-    // which lies more than 1536 below the row max (table entry 1537 = 0) whenever the row max
-    // exceeds kMasked + 1536.  In waves with a row whose every score is near -32768, the tiles
-    // holding keys outside [sequence start, query] (the diagonal tile, and the first one when the
-    // sequence does not start on a 32-row boundary) test the keys; the branch is uniform per tile.
+    // The packed scores become packed byte offsets 4 min(rowmax - s, 1537) into the exp table
+    // (rowmax - s lies in [0, 65535], so 16-bit lanes hold it and the shifted offset), 3 packed
+    // operations per 2 keys, once for both lookup passes.  A masked key holds score kMasked, which
+    // lies more than 1536 below the row max (table entry 1537 = 0) whenever the row max exceeds
+    // kMasked + 1536.  In waves with a row whose every score is near -32768, the tiles holding keys
+    // outside [sequence start, query] (the diagonal tile, and the first one when the sequence does
+    // not start on a 32-row boundary) test the keys; the branch is uniform per tile.
     const bool clean = __all(rowmax > kMasked + kDMax);
-    auto edge = [&](int t) __attribute__((always_inline)) {
-      return !clean && (32 * (g0 + t) < s0 || 32 * (g0 + t) + 31 > q0);
-    };
+    const u16x2 rm2 = (u16x2)(unsigned short)rowmax, cap2 = (u16x2)(unsigned short)(kDMax + 1);
+#pragma unroll
+    for (int t = 0; t < NKT; ++t)
+      if (t < ntile) {
+        if (!clean && (32 * (g0 + t) < s0 || 32 * (g0 + t) + 31 > q0)) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            uint32_t off[2];
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+              const int j = 2 * i + b, key = 32 * (g0 + t) + 16 * h + j;
+              const int32_t sj = b ? (int32_t)pk[t][i] >> 16 : (int32_t)(pk[t][i] << 16) >> 16;
+              off[b] = 4u * (uint32_t)(key < s0 || key > qi ? kDMax + 1 : min(rowmax - sj, kDMax + 1));
+            }
+            pk[t][i] = off[0] | (off[1] << 16);
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            u16x2 d = rm2 - __builtin_bit_cast(u16x2, pk[t][i]);
+            d = __builtin_elementwise_min(d, cap2) << (u16x2)(unsigned short)2;
+            pk[t][i] = __builtin_bit_cast(uint32_t, d);
+          }
+        }
+      }
     auto ex = [&](int t, int j) __attribute__((always_inline)) -> int32_t {
-      return etab[min(rowmax - unpack(t, j), kDMax + 1)];
+      const uint32_t p = pk[t][j >> 1], off = (j & 1) ? p >> 16 : p & 0xFFFFu;
+      return *(const int32_t*)((const char*)etab + off);
     };
     // Z: e <= 2^30, so sums of three fit uint32
     uint64_t Z = 0;
@@ -1342,13 +1371,8 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
     for (int t = 0; t < NKT; ++t)
       if (t < ntile) {
         uint32_t ev[16];
-        if (edge(t)) {
 #pragma unroll
-          for (int j = 0; j < 16; ++j) ev[j] = expo(g0 + t, j, unpack(t, j), rowmax);
-        } else {
-#pragma unroll
-          for (int j = 0; j < 16; ++j) ev[j] = ex(t, j);
-        }
+        for (int j = 0; j < 16; ++j) ev[j] = ex(t, j);
 #pragma unroll
         for (int j = 0; j < 15; j += 3) Z += ev[j] + ev[j + 1] + ev[j + 2];
         Z += ev[15];
@@ -1363,13 +1387,8 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
           load_v(g0 + t, vf[0]);
         }
         int32_t ev[16];
-        if (edge(t)) {
 #pragma unroll
-          for (int j = 0; j < 16; ++j) ev[j] = expo(g0 + t, j, unpack(t, j), rowmax);
-        } else {
-#pragma unroll
-          for (int j = 0; j < 16; ++j) ev[j] = ex(t, j);
-        }
+        for (int j = 0; j < 16; ++j) ev[j] = ex(t, j);
         pv(vf[ahead ? t & 1 : 0], ev);
       }
   } else {

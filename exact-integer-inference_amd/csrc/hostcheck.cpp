@@ -272,6 +272,48 @@ int64_t eii_host_attn_model(uint64_t seed, int plant) {
   return bad;
 }
 
+// Score digits (attn_q_digits): every int16 query element is 256 (qh + qx) + ql with int8 digits
+// and qx in {0, 1}, every key element 256 kh + kl + 128; on random and extreme 64-dimension rows the
+// digit sums the MFMAs form give q . k exactly, and lo = 256 A8 + A0 + 128 sum q + 2^(sh - 1) (the
+// kernel's int32 piece) stays inside int32.  Returns the number of mismatches (plant 1: qx dropped).
+int64_t eii_host_attn_digits(uint64_t seed, int plant) {
+  int64_t bad = 0;
+  for (int q = -32768; q <= 32767; ++q) {
+    QDigits d = attn_q_digits(q);
+    if (plant == 1) d.qx = 0;
+    bad += d.ql < -128 || d.ql > 127 || d.qh < -128 || d.qh > 127 || d.qx < 0 || d.qx > 1;
+    bad += 256 * (d.qh + d.qx) + d.ql != q;
+  }
+  for (int k = -32768; k <= 32767; ++k) {
+    const int kh = k >> 8, kl = (k & 255) - 128;
+    bad += kh < -128 || kh > 127 || 256 * kh + kl + 128 != k;
+  }
+  uint64_t r = seed;
+  int q[64], k[64];
+  for (int t = 0; t < 4000; ++t) {
+    for (int d = 0; d < 64; ++d) {
+      const int mode = t % 8;   // random, and rows at the int16 extremes
+      q[d] = mode == 1 ? 32767 : mode == 2 ? -32768 : mode == 3 ? 32640 + (int)(next_rand(r) % 128) : (int)(int16_t)next_rand(r);
+      k[d] = mode == 1 || mode == 5 ? 32767 : mode == 2 || mode == 6 ? -32768 : (int)(int16_t)next_rand(r);
+    }
+    int64_t truth = 0, A16 = 0, A8 = 0, A0 = 0, sq = 0;
+    for (int d = 0; d < 64; ++d) {
+      truth += (int64_t)q[d] * k[d];
+      QDigits g = attn_q_digits(q[d]);
+      if (plant == 1) g.qx = 0;
+      const int kh = k[d] >> 8, kl = (k[d] & 255) - 128;
+      A16 += (int64_t)(g.qh + g.qx) * kh;
+      A8 += (int64_t)(g.qh + g.qx) * kl + (int64_t)g.ql * kh;
+      A0 += (int64_t)g.ql * kl;
+      sq += q[d];
+    }
+    bad += 65536 * A16 + 256 * A8 + A0 + 128 * sq != truth;
+    const int64_t lo = 256 * A8 + A0 + 128 * sq + ((int64_t)1 << 29);
+    bad += lo < INT32_MIN || lo > INT32_MAX || A16 < INT32_MIN || A16 > INT32_MAX;
+  }
+  return bad;
+}
+
 // Fragment order of the weights: element (n, k) lands where the swizzle kernel's thread for
 // (block n / 32, slice k / 32, lane 32 ((k % 32) / 16) + n % 32) writes byte k % 16, and the map is
 // one-to-one over the padded matrix.  Returns the number of mismatches.

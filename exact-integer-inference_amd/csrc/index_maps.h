@@ -108,5 +108,17 @@ EII_HD size_t w_fo_offset(size_t n, size_t k, size_t kslices) {
 // which is the B-operand layout of the P.V product (bytes j = keys 16 h + j).
 EII_HD int attn_key_perm(int i) { return 16 * ((i >> 2) & 1) + 4 * (i >> 3) + (i & 3); }
 
+// Int8 digits of the score MFMAs.  A query element is q = 256 (qh + qx) + ql with ql its low byte
+// read as int8, qh = min((q + 128) >> 8, 127) and qx = ((q + 128) >> 8) - qh, which is 1 only for
+// q >= 32640; a key element is k = 256 kh + kl + 128 with kh its signed high byte and kl its low
+// byte - 128 (the V^T planes' form).  Then, summed over the 64 dimensions,
+//   q . k = 65536 sum (qh + qx) kh + 256 sum ((qh + qx) kl + ql kh) + sum ql kl + 128 sum q,
+// where the last term is one constant per query: no per-key sum is needed.
+struct QDigits { int ql, qh, qx; };
+EII_HD QDigits attn_q_digits(int q) {
+  const int hd = (q + 128) >> 8, h = hd < 127 ? hd : 127;
+  return QDigits{(int)(int8_t)(uint8_t)(q & 0xFF), h, hd - h};
+}
+
 }  // namespace idx
 }  // namespace eii

@@ -991,8 +991,8 @@ __global__ __launch_bounds__(256) void silu_kernel(const int16_t* gu, int M, con
 // table.  The longest query tiles are dispatched first.
 //
 // Scores run on v_mfma_i32_32x32x32_i8 as S^T[key][query] = K . Q^T over the head dimension (two
-// K-steps of 32) with q = 256 QH + (QL' + 128), QL' = low byte - 128, QH = signed high byte, and
-// k likewise.  A-operand row i carries key pi(i) = 16 ((i >> 2) & 1) + 4 (i >> 3) + (i & 3) of the
+// K-steps of 32) with k = 256 KH + (KL' + 128), KL' = low byte - 128, KH = signed high byte, and q
+// likewise or in the digits of attn_q_digits (index_maps.h).  A-operand row i carries key pi(i) = 16 ((i >> 2) & 1) + 4 (i >> 3) + (i & 3) of the
 // key tile, the key that output row i denotes, so lane 32 h + c ends with query c and keys
 // 16 h + j (output register j) of the tile: 16 consecutive keys of one query, which is the
 // B-operand layout of ctx^T[d][query] = sum_key V^T[d][key] P^T[key][query] with operand byte j =
@@ -1000,6 +1000,9 @@ __global__ __launch_bounds__(256) void silu_kernel(const int16_t* gu, int M, con
 // blocks aligned to row 0 of the batch; keys outside [sequence start, query] are masked.
 //
 // Exact sums (all partial MFMA sums fit int32):
+//   sum_d q k = 65536 S_HH + 256 (S_HL + S_LH) + S_LL + 128 sum_d q
+// with q in the digits of attn_q_digits (S_HH and S_HL with the high digits qh + qx), so the key
+// rows need no sums; with q in k's form instead (the register-resident scores),
 //   sum_d q k = 65536 S_HH + 256 (S_HL + S_LH) + S_LL + 128 (sum_d q + sum_d k) - 2^20
 //   sum_key P v = 65536 C_1H + 256 (C_1L + C_0H) + C_0L + 128 sum_key P
 // where P = 256 R1 + P0 with P0 = sext(P & 255) and R1 = (P + 128) >> 8 in [0, 256] (R1 goes
@@ -1020,11 +1023,13 @@ __device__ __forceinline__ int32_t sum16x8(u32x4 d, int32_t s = 0) {   // s + th
 template <int OB, int NKT, int WPG>
 __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) void attn_kernel(AttnArgs a) {
   static_assert(WPG == 1 || WPG == 4, "one wave per workgroup, or 4 independent waves");
-  __shared__ int32_t etab[kDMax + 2];                             // exp table, etab[1537] = 0
+  __shared__ int32_t etab[kDMax + 2];                              // exp table, etab[1537] = 0
   __shared__ __attribute__((aligned(16))) int32_t sklw[WPG][32];   // per wave: 128 * sum_d k per key
+  __shared__ __attribute__((aligned(16))) v4i qxw[NKT == 0 ? WPG : 1][2][64];   // per wave: qx digits
 
   const int tid = threadIdx.x, lane = tid & 63, c = lane & 31, h = lane >> 5;
   int32_t* const skl = sklw[WPG == 1 ? 0 : tid >> 6];
+  v4i (*const qxs)[64] = qxw[NKT == 0 && WPG > 1 ? tid >> 6 : 0];
   // this wave's (sequence, query head 3 kvg + w, query tile qt)
   int seq, kvg, w, qt;
   bool idle = false;
@@ -1057,10 +1062,16 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
   const int sh = a.shift_s;
   const int vts = vt_stride_for(a.M);
 
-  // B operand: query qi (rows past the sequence read its last row), d = 32 s + 16 h + 0..15
+  // B operand: query qi (rows past the sequence read its last row), d = 32 s + 16 h + 0..15.  The
+  // recomputing passes (kDig) take q as the digits of attn_q_digits (ql, qh; qx in LDS, read only in
+  // waves where some q >= 32640), which spares them the per-key sums of k; with the scores held in
+  // registers q takes k's form (low byte - 128, signed high byte) and the key sums go through LDS
+  // (fewer registers and no branch in the one score pass; measured faster there)
+  constexpr bool kDig = NKT == 0;
   v4i ql[2], qh[2];
   int32_t cq;
-  {
+  bool qbig = false;
+  if constexpr (!kDig) {
     const int16_t* qp = a.qkv + (size_t)min(qi, qlast) * kQKVN + hh * 64 + 16 * h;
     int32_t sum = 0;
 #pragma unroll
@@ -1074,6 +1085,32 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
     }
     sum += __shfl_xor(sum, 32);
     cq = 128 * sum - (1 << 20) + (1 << (sh - 1));   // with the rounding offset of RS(., sh)
+  } else {
+    const int16_t* qp = a.qkv + (size_t)min(qi, qlast) * kQKVN + hh * 64 + 16 * h;
+    int32_t sum = 0;
+    uint32_t anyx = 0;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const u32x4 d0 = *(const u32x4*)(qp + 32 * s), d1 = *(const u32x4*)(qp + 32 * s + 8);
+      uint32_t wl[4] = {0, 0, 0, 0}, wh[4] = {0, 0, 0, 0}, wx[4] = {0, 0, 0, 0};
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const uint32_t wd = e < 8 ? d0[e >> 1] : d1[(e - 8) >> 1];
+        const QDigits g = attn_q_digits((e & 1) ? (int32_t)wd >> 16 : (int32_t)(wd << 16) >> 16);
+        wl[e >> 2] |= ((uint32_t)g.ql & 0xFFu) << (8 * (e & 3));
+        wh[e >> 2] |= ((uint32_t)g.qh & 0xFFu) << (8 * (e & 3));
+        wx[e >> 2] |= (uint32_t)g.qx << (8 * (e & 3));
+      }
+      ql[s] = v4i{(int)wl[0], (int)wl[1], (int)wl[2], (int)wl[3]};
+      qh[s] = v4i{(int)wh[0], (int)wh[1], (int)wh[2], (int)wh[3]};
+      qxs[s][lane] = v4i{(int)wx[0], (int)wx[1], (int)wx[2], (int)wx[3]};
+      anyx |= wx[0] | wx[1] | wx[2] | wx[3];
+      sum = sum16x8(d1, sum16x8(d0, sum));
+    }
+    qbig = __any(anyx != 0);
+    sum += __shfl_xor(sum, 32);
+    cq = 128 * sum + (1 << (sh - 1));   // with the rounding offset of RS(., sh)
+    __builtin_amdgcn_wave_barrier();
   }
 
   // K rows of key tile g for this lane (row pi(c) of the tile, d = 32 s + 16 h + 0..15), loaded
@@ -1100,11 +1137,13 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
                   (int)lo_bytes16(d1[2], d1[3])};
       kh[s] = v4i{(int)hi_bytes16(d0[0], d0[1]), (int)hi_bytes16(d0[2], d0[3]), (int)hi_bytes16(d1[0], d1[1]),
                   (int)hi_bytes16(d1[2], d1[3])};
-      ks = sum16x8(d1, sum16x8(d0, ks));
+      if constexpr (!kDig) ks = sum16x8(d1, sum16x8(d0, ks));
     }
-    ks += __shfl_xor(ks, 32);
-    skl[pic] = 128 * ks;   // lanes c and c + 32 store the same value
-    __builtin_amdgcn_wave_barrier();
+    if constexpr (!kDig) {
+      ks += __shfl_xor(ks, 32);
+      skl[pic] = 128 * ks;   // lanes c and c + 32 store the same value
+      __builtin_amdgcn_wave_barrier();
+    }
     v16i a16 = v16i{}, a8 = v16i{}, a0 = v16i{};
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
@@ -1113,14 +1152,30 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
       a8 = mfma32(kl[s], qh[s], a8);
       a0 = mfma32(kl[s], ql[s], a0);
     }
-    const v4i* kk = (const v4i*)&skl[16 * h];
-    const v4i k4[4] = {kk[0], kk[1], kk[2], kk[3]};
-    __builtin_amdgcn_wave_barrier();
-    int32_t lo[16], wv[16];
+    if (kDig && qbig) {   // the qx digits of queries >= 32640
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      lo[j] = a8[j] * 256 + a0[j] + k4[j >> 2][j & 3] + cq;
-      wv[j] = a16[j] + (lo[j] >> 16);
+      for (int s = 0; s < 2; ++s) {
+        const v4i qx = qxs[s][lane];
+        a16 = mfma32(kh[s], qx, a16);
+        a8 = mfma32(kl[s], qx, a8);
+      }
+    }
+    int32_t lo[16], wv[16];
+    if constexpr (!kDig) {
+      const v4i* kk = (const v4i*)&skl[16 * h];
+      const v4i k4[4] = {kk[0], kk[1], kk[2], kk[3]};
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        lo[j] = a8[j] * 256 + a0[j] + k4[j >> 2][j & 3] + cq;
+        wv[j] = a16[j] + (lo[j] >> 16);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        lo[j] = a8[j] * 256 + a0[j] + cq;
+        wv[j] = a16[j] + (lo[j] >> 16);
+      }
     }
     // the shift is uniform: one branch per tile
     if (sh >= 16) {

@@ -110,6 +110,8 @@ def load_hostcheck():
     lib.eii_host_gemm_model.argtypes = [i32, i32, i32, i32, i32, i32, C.c_uint64, i32, vp]
     lib.eii_host_attn_model.restype = C.c_int64
     lib.eii_host_attn_model.argtypes = [C.c_uint64, i32]
+    lib.eii_host_attn_digits.restype = C.c_int64
+    lib.eii_host_attn_digits.argtypes = [C.c_uint64, i32]
     lib.eii_host_wfrag_model.restype = C.c_int64
     lib.eii_host_wfrag_model.argtypes = [i32, i32]
     return lib

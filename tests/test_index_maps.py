@@ -76,6 +76,12 @@ def test_attention_layouts(hc):
     assert hc.eii_host_attn_model(7, 1) > 0           # planted: key order without the row-group swap
 
 
+def test_attention_score_digits(hc):
+    # every int16 query and key element, and 4000 random and extreme 64-dimension rows
+    assert hc.eii_host_attn_digits(11, 0) == 0
+    assert hc.eii_host_attn_digits(11, 1) > 0         # planted: the extra 0/1 digit of q >= 32640 dropped
+
+
 @pytest.mark.parametrize("N,K", [(576, 576), (960, 576), (100, 64), (33, 1536)])
 def test_weight_fragment_order(hc, N, K):
     assert hc.eii_host_wfrag_model(N, K) == 0

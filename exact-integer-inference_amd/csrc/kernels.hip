@@ -1320,15 +1320,26 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
   VFrag vf[ahead ? 2 : 1];
   // every pass recomputes the scores; the exp lookups test keys only in waves with a row max
   // near -32768 (see the register-resident passes below)
+  // The row-max and exp-sum passes load the K rows of tile t + 1 while tile t computes (two tiles
+  // per iteration, so the buffer of each is a compile-time choice); the P.V pass, whose registers
+  // hold the context sums, loads each tile's K and V at its start.
   auto recompute_passes = [&]() __attribute__((always_inline)) {
+    KRows kb[2];
     rowmax = kMasked;
+    load_k(g0, kb[0]);
 #pragma unroll 1
-    for (int t = 0; t < ntile; ++t) {
-      int32_t sc[16];
-      load_k(g0 + t, kr[0]);
-      scores(g0 + t, kr[0], sc);
+    for (int t0 = 0; t0 < ntile; t0 += 2) {
 #pragma unroll
-      for (int j = 0; j < 16; ++j) rowmax = max(rowmax, sc[j]);
+      for (int u = 0; u < 2; ++u) {
+        const int t = t0 + u;
+        if (t < ntile) {
+          if (t + 1 < ntile) load_k(g0 + t + 1, kb[u ^ 1]);
+          int32_t sc[16];
+          scores(g0 + t, kb[u], sc);
+#pragma unroll
+          for (int j = 0; j < 16; ++j) rowmax = max(rowmax, sc[j]);
+        }
+      }
     }
     rowmax = max(rowmax, __shfl_xor(rowmax, 32));
     auto passes = [&](auto CLEAN) __attribute__((always_inline)) {
@@ -1337,14 +1348,21 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
         else return (uint32_t)expo(g0 + t, j, s, rowmax);
       };
       uint64_t Z = 0;   // e <= 2^30: sums of three fit uint32
+      load_k(g0, kb[0]);
 #pragma unroll 1
-      for (int t = 0; t < ntile; ++t) {
-        int32_t sc[16];
-        load_k(g0 + t, kr[0]);
-        scores(g0 + t, kr[0], sc);
+      for (int t0 = 0; t0 < ntile; t0 += 2) {
 #pragma unroll
-        for (int j = 0; j < 15; j += 3) Z += ex(t, j, sc[j]) + ex(t, j + 1, sc[j + 1]) + ex(t, j + 2, sc[j + 2]);
-        Z += ex(t, 15, sc[15]);
+        for (int u = 0; u < 2; ++u) {
+          const int t = t0 + u;
+          if (t < ntile) {
+            if (t + 1 < ntile) load_k(g0 + t + 1, kb[u ^ 1]);
+            int32_t sc[16];
+            scores(g0 + t, kb[u], sc);
+#pragma unroll
+            for (int j = 0; j < 15; j += 3) Z += ex(t, j, sc[j]) + ex(t, j + 1, sc[j + 1]) + ex(t, j + 2, sc[j + 2]);
+            Z += ex(t, 15, sc[15]);
+          }
+        }
       }
       set_z((int64_t)Z);
 #pragma unroll 1

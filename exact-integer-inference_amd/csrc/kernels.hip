@@ -1127,7 +1127,11 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
   };
   // Scores SAT16(RS(q.k, sh)) of key tile g for this lane's query, keys 16 h + j.  The sum
   // acc + 2^(sh-1) = 65536 wv + lo16 with lo16 in [0, 65536) is evaluated in int32 pieces.
-  auto scores = [&](int g, const KRows& kr, int32_t (&sc)[16]) __attribute__((always_inline)) {
+  // RAW (shift >= 16 only): sc = the high parts wv, whose shifted and clamped values are the
+  // scores; the row max of the scores is that of wv, shifted and clamped (both maps are monotone)
+  auto scores = [&](int g, const KRows& kr, int32_t (&sc)[16], auto RAW) __attribute__((always_inline)) {
+    constexpr bool raw = decltype(RAW)::value;
+    constexpr int32_t masked = raw ? INT32_MIN : kMasked;
     v4i kl[2], kh[2];
     int32_t ks = 0;
 #pragma unroll
@@ -1178,7 +1182,10 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
       }
     }
     // the shift is uniform: one branch per tile
-    if (sh >= 16) {
+    if constexpr (raw) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) sc[j] = wv[j];
+    } else if (sh >= 16) {
 #pragma unroll
       for (int j = 0; j < 16; ++j) sc[j] = min(max(wv[j] >> (sh - 16), -32768), 32767);
     } else {
@@ -1192,15 +1199,17 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
       const int last = qi - 32 * g - 16 * h;
 #pragma unroll
       for (int j = 0; j < 16; ++j)
-        if (j > last) sc[j] = kMasked;
+        if (j > last) sc[j] = masked;
     }
     if (32 * g < s0) {
       const int first = s0 - 32 * g - 16 * h;
 #pragma unroll
       for (int j = 0; j < 16; ++j)
-        if (j < first) sc[j] = kMasked;
+        if (j < first) sc[j] = masked;
     }
   };
+  using Raw = std::true_type;
+  using Full = std::false_type;
   // e = E[rowmax - s] for d <= 1536, else 0; masked keys 0
   auto expo = [&](int g, int j, int32_t s, int32_t rowmax) __attribute__((always_inline)) -> int32_t {
     const int32_t e = etab[min(rowmax - s, kDMax + 1)];
@@ -1325,22 +1334,27 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
   // hold the context sums, loads each tile's K and V at its start.
   auto recompute_passes = [&]() __attribute__((always_inline)) {
     KRows kb[2];
-    rowmax = kMasked;
-    load_k(g0, kb[0]);
+    auto max_pass = [&](auto RAW) __attribute__((always_inline)) {
+      int32_t m = INT32_MIN;
+      load_k(g0, kb[0]);
 #pragma unroll 1
-    for (int t0 = 0; t0 < ntile; t0 += 2) {
+      for (int t0 = 0; t0 < ntile; t0 += 2) {
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int t = t0 + u;
-        if (t < ntile) {
-          if (t + 1 < ntile) load_k(g0 + t + 1, kb[u ^ 1]);
-          int32_t sc[16];
-          scores(g0 + t, kb[u], sc);
+        for (int u = 0; u < 2; ++u) {
+          const int t = t0 + u;
+          if (t < ntile) {
+            if (t + 1 < ntile) load_k(g0 + t + 1, kb[u ^ 1]);
+            int32_t sc[16];
+            scores(g0 + t, kb[u], sc, RAW);
 #pragma unroll
-          for (int j = 0; j < 16; ++j) rowmax = max(rowmax, sc[j]);
+            for (int j = 0; j < 16; ++j) m = max(m, sc[j]);
+          }
         }
       }
-    }
+      return m;
+    };
+    if (sh >= 16) rowmax = min(max(max_pass(Raw{}) >> (sh - 16), -32768), 32767);
+    else rowmax = max_pass(Full{});
     rowmax = max(rowmax, __shfl_xor(rowmax, 32));
     auto passes = [&](auto CLEAN) __attribute__((always_inline)) {
       auto ex = [&](int t, int j, int32_t s) __attribute__((always_inline)) -> uint32_t {
@@ -1357,7 +1371,7 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
           if (t < ntile) {
             if (t + 1 < ntile) load_k(g0 + t + 1, kb[u ^ 1]);
             int32_t sc[16];
-            scores(g0 + t, kb[u], sc);
+            scores(g0 + t, kb[u], sc, Full{});
 #pragma unroll
             for (int j = 0; j < 15; j += 3) Z += ex(t, j, sc[j]) + ex(t, j + 1, sc[j + 1]) + ex(t, j + 2, sc[j + 2]);
             Z += ex(t, 15, sc[15]);
@@ -1370,7 +1384,7 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
         int32_t sc[16];
         load_k(g0 + t, kr[0]);
         load_v(g0 + t, vf[0]);
-        scores(g0 + t, kr[0], sc);
+        scores(g0 + t, kr[0], sc, Full{});
 #pragma unroll
         for (int j = 0; j < 16; ++j) sc[j] = (int32_t)ex(t, j, sc[j]);
         pv(vf[0], sc);
@@ -1392,7 +1406,7 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
           load_k(g0 + t, kr[0]);
         }
         int32_t sc[16];
-        scores(g0 + t, kr[ahead ? t & 1 : 0], sc);
+        scores(g0 + t, kr[ahead ? t & 1 : 0], sc, Full{});
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           pk[t][i] = ((uint32_t)sc[2 * i] & 0xFFFFu) | ((uint32_t)sc[2 * i + 1] << 16);

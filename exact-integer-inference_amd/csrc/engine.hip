@@ -616,12 +616,13 @@ int run_block(eii_model* m, int l, int32_t* x, int M, int nseq, int max_T, const
         g.ldc = kv->kv->cap * kQKVN;
       }
       HIPCHK(gemm(g, hb, EPI_QKV, s));
-      // decoding: the new rows join the cache; when this step's attention reads the V^T planes,
-      // the positions that earlier single-token steps left out get theirs first
+      // decoding: the new rows join the cache, then (when this step's attention reads them) the
+      // V^T planes of every position not yet covered, the new ones included, in one pass whose
+      // stores run along the positions of each plane row
       if (kv && !direct) {
         eii_kv* c = kv->kv;
-        if (kv->vt) HIPCHK(kv_build_vt(c->qkv[l], nseq, c->cap, c->vt_len, kv->p0, c->vt[l], s));
-        HIPCHK(kv_append(m->qkv, nseq, kv->T_new, c->cap, kv->p0, c->qkv[l], kv->vt ? c->vt[l] : nullptr, s));
+        HIPCHK(kv_append(m->qkv, nseq, kv->T_new, c->cap, kv->p0, c->qkv[l], s));
+        if (kv->vt) HIPCHK(kv_build_vt(c->qkv[l], nseq, c->cap, c->vt_len, kv->p0 + kv->T_new, c->vt[l], s));
       }
     } else {
       HIPCHK(gemm(g, hb, EPI_REQ16, s));

@@ -156,12 +156,11 @@ inline int attn_key_tiles(int s0, int T) { return ((s0 + T - 1) >> 5) - (s0 >> 5
 hipError_t attention(const AttnArgs& a, hipStream_t s);
 
 // KV cache append: rows b T_new + i of qkv [B T_new, 960] go to row b cap + p0 + i of the cache
-// rows and, for the v columns, to the cache's V^T limb planes (vt_stride_for(B cap)) unless
-// cache_vt is null
-hipError_t kv_append(const int16_t* qkv, int B, int T_new, int cap, int p0, int16_t* cache_qkv, uint8_t* cache_vt,
-                     hipStream_t s);
-// V^T planes of the cached positions [from, to) of every sequence, rebuilt from the cached v rows
-// (single-token appends that the one-query decoding kernel serves leave them out)
+// rows (the V^T planes: kv_build_vt)
+hipError_t kv_append(const int16_t* qkv, int B, int T_new, int cap, int p0, int16_t* cache_qkv, hipStream_t s);
+// V^T planes (vt_stride_for(B cap)) of the cached positions [from, to) of every sequence, built
+// from the cached v rows (single-token appends that the one-query decoding kernel serves leave
+// them out until a step needs them)
 hipError_t kv_build_vt(const int16_t* cache_qkv, int B, int cap, int from, int to, uint8_t* cache_vt, hipStream_t s);
 // longest cache the one-query decoding attention serves (its scores of 3 heads sit in LDS); longer
 // caches take the tiled kernel, which reads the V^T planes

@@ -1883,49 +1883,59 @@ hipError_t attention(const AttnArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
-// KV cache append: thread = (new row, one of the 960 columns); the v columns also write their two
-// V^T limb bytes (low byte - 128, signed high byte) at the row's cache column
+// KV cache append: thread = (new row, 8 consecutive of its 960 columns), one 16-byte copy
 __global__ __launch_bounds__(256) void kv_append_kernel(const int16_t* qkv, int B, int T_new, int cap, int p0,
-                                                         int16_t* cache, uint8_t* vt, int stride) {
+                                                         int16_t* cache) {
+  constexpr int kC8 = kQKVN / 8;
   const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= (size_t)B * T_new * kQKVN) return;
-  const int r = (int)(i / kQKVN), col = (int)(i % kQKVN), b = r / T_new, t = r % T_new;
+  if (i >= (size_t)B * T_new * kC8) return;
+  const int r = (int)(i / kC8), c8 = (int)(i % kC8), b = r / T_new, t = r % T_new;
   const size_t crow = (size_t)b * cap + p0 + t;
-  const int16_t v = qkv[i];
-  cache[crow * kQKVN + col] = v;
-  if (vt && col >= kD + 192) {
-    const size_t d = col - kD - 192;
-    vt[d * stride + crow] = (uint8_t)((uint32_t)v ^ 0x80u);
-    vt[(size_t)192 * stride + d * stride + crow] = (uint8_t)((uint32_t)v >> 8);
+  *(int4*)(cache + crow * kQKVN + 8 * c8) = *(const int4*)(qkv + (size_t)r * kQKVN + 8 * c8);
+}
+
+// V^T planes of cached positions [from, to) of every sequence.  Workgroup = (sequence, 64
+// positions): the v columns of its rows come in as whole rows and pass through LDS (rows padded to
+// 97 dwords, so the reads of one column at 64 consecutive positions hit 64 banks), then each plane
+// row's bytes for those positions leave as one contiguous run.
+__global__ __launch_bounds__(256) void kv_vt_kernel(const int16_t* cache, int cap, int from, int to, int nchunk,
+                                                    uint8_t* vt, int stride) {
+  __shared__ __attribute__((aligned(16))) int16_t tv[64][194];
+  const int b = blockIdx.x / nchunk, t0 = from + 64 * (blockIdx.x % nchunk), n = min(64, to - t0);
+  const size_t row0 = (size_t)b * cap + t0;
+  for (int i = threadIdx.x; i < 64 * 24; i += 256) {   // 24 x 8 v values per row
+    const int p = i / 24, q = i % 24;
+    if (p < n) {
+      const int4 v = *(const int4*)(cache + (row0 + p) * kQKVN + kD + 192 + 8 * q);
+      int32_t* dst = (int32_t*)&tv[p][8 * q];
+      dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;
+    }
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < 192 * 64; i += 256) {
+    const int p = i & 63, d = i >> 6;
+    if (p < n) {
+      const uint32_t v = (uint16_t)tv[p][d];
+      uint8_t* o = vt + (size_t)d * stride + row0 + p;
+      o[0] = (uint8_t)(v ^ 0x80u);
+      o[(size_t)192 * stride] = (uint8_t)(v >> 8);
+    }
   }
 }
 
-// V^T planes of cached positions [from, to) of every sequence, from the cached v rows: thread =
-// (plane, d, sequence, position), positions fastest, so each store run is contiguous
-__global__ __launch_bounds__(256) void kv_vt_kernel(const int16_t* cache, int B, int cap, int from, int to,
-                                                    uint8_t* vt, int stride) {
-  const int n = to - from;
-  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= (size_t)2 * 192 * B * n) return;
-  const int t = (int)(i % n), b = (int)(i / n % B), d = (int)(i / ((size_t)n * B) % 192), l = (int)(i / ((size_t)n * B * 192));
-  const size_t crow = (size_t)b * cap + from + t;
-  const uint32_t v = (uint16_t)cache[crow * kQKVN + kD + 192 + d];
-  vt[(size_t)l * 192 * stride + (size_t)d * stride + crow] = (uint8_t)(l ? v >> 8 : v ^ 0x80u);
-}
-
-hipError_t kv_append(const int16_t* qkv, int B, int T_new, int cap, int p0, int16_t* cache_qkv, uint8_t* cache_vt,
-                     hipStream_t s) {
+hipError_t kv_append(const int16_t* qkv, int B, int T_new, int cap, int p0, int16_t* cache_qkv, hipStream_t s) {
   if (B <= 0 || T_new <= 0 || p0 < 0 || p0 + T_new > cap) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(kv_append_kernel, dim3(blocks_for((size_t)B * T_new * kQKVN)), dim3(256), 0, s, qkv, B, T_new,
-                     cap, p0, cache_qkv, cache_vt, vt_stride_for(B * cap));
+  hipLaunchKernelGGL(kv_append_kernel, dim3(blocks_for((size_t)B * T_new * (kQKVN / 8))), dim3(256), 0, s, qkv, B,
+                     T_new, cap, p0, cache_qkv);
   return hipGetLastError();
 }
 
 hipError_t kv_build_vt(const int16_t* cache_qkv, int B, int cap, int from, int to, uint8_t* cache_vt, hipStream_t s) {
   if (B <= 0 || from < 0 || to > cap || from > to) return hipErrorInvalidValue;
   if (from == to) return hipSuccess;
-  hipLaunchKernelGGL(kv_vt_kernel, dim3(blocks_for((size_t)2 * 192 * B * (to - from))), dim3(256), 0, s, cache_qkv, B,
-                     cap, from, to, cache_vt, vt_stride_for(B * cap));
+  const int nchunk = (to - from + 63) / 64;
+  hipLaunchKernelGGL(kv_vt_kernel, dim3((unsigned)((size_t)B * nchunk)), dim3(256), 0, s, cache_qkv, cap, from, to,
+                     nchunk, cache_vt, vt_stride_for(B * cap));
   return hipGetLastError();
 }
 

@@ -1020,12 +1020,18 @@ __device__ __forceinline__ int32_t sum16x8(u32x4 d, int32_t s = 0) {   // s + th
   return s;
 }
 
-template <int OB, int NKT, int WPG>
+template <int OB, int NKT, int WPG, int KS = 1>
 __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) void attn_kernel(AttnArgs a) {
-  static_assert(WPG == 1 || WPG == 4, "one wave per workgroup, or 4 independent waves");
+  static_assert(WPG == 1 || WPG == 4, "one wave per workgroup, or 4 waves");
+  static_assert(KS == 1 || (KS == WPG && NKT > 0), "key tiles split over the waves of one task");
   __shared__ int32_t etab[kDMax + 2];                              // exp table, etab[1537] = 0
   __shared__ __attribute__((aligned(16))) int32_t sklw[WPG][32];   // per wave: 128 * sum_d k per key
   __shared__ __attribute__((aligned(16))) v4i qxw[NKT == 0 ? WPG : 1][2][64];   // per wave: qx digits
+  // KS > 1: the waves' partial row maxima, exp sums, context sums and probability sums
+  __shared__ int32_t xmax[KS][32];
+  __shared__ uint64_t xz[KS][32];
+  __shared__ int32_t xc[KS > 1 ? 6 * 16 : 1][64];
+  __shared__ int32_t xsp[KS > 1 ? 64 : 1];
 
   const int tid = threadIdx.x, lane = tid & 63, c = lane & 31, h = lane >> 5;
   int32_t* const skl = sklw[WPG == 1 ? 0 : tid >> 6];
@@ -1033,7 +1039,7 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
   // this wave's (sequence, query head 3 kvg + w, query tile qt)
   int seq, kvg, w, qt;
   bool idle = false;
-  if constexpr (WPG == 1) {
+  if constexpr (WPG == 1 || KS > 1) {
     seq = blockIdx.x;
     kvg = blockIdx.y / 3;
     w = blockIdx.y % 3;
@@ -1050,7 +1056,7 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
   }
   const int s0 = a.seq_off[seq], T = a.kv_len ? a.kv_len : a.seq_off[seq + 1] - s0;
   idle = idle || 32 * qt >= T;
-  if (WPG == 1 && idle) return;
+  if ((WPG == 1 || KS > 1) && idle) return;   // uniform over the workgroup
   for (int i = tid; i < kDMax + 2; i += 64 * WPG) etab[i] = i <= kDMax ? a.exp_tab[i] : 0;
   __syncthreads();
   if (idle) return;   // (no workgroup barrier follows)
@@ -1314,8 +1320,8 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
       }
     }
   };
-  auto set_z = [&](int64_t Z) __attribute__((always_inline)) {
-    Z += __shfl_xor(Z, 32);
+  auto set_z = [&](int64_t Z, bool halves = true) __attribute__((always_inline)) {
+    if (halves) Z += __shfl_xor(Z, 32);   // the two lane halves' keys (already added: false)
     const double Zd = (double)Z;   // Z < 2^43: exact
     Zs = Zd * 0x1p-16;
     rZs = (1.0 / Zd) * 65536.0;
@@ -1324,7 +1330,7 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
 
   int32_t rowmax = kMasked;
   // with up to 5 key tiles the registers hold K and V one tile ahead of their use as well
-  constexpr bool ahead = NKT > 0 && NKT <= 5;
+  constexpr bool ahead = NKT > 0 && NKT <= 5 && KS == 1;
   KRows kr[ahead ? 2 : 1];
   VFrag vf[ahead ? 2 : 1];
   // every pass recomputes the scores; the exp lookups test keys only in waves with a row max
@@ -1394,19 +1400,24 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
     else passes(std::false_type{});
   };
   if constexpr (NKT > 0) {
-    uint32_t pk[NKT][8];   // packed int16 scores
+    // KS > 1: wave ks of the task takes key tiles ks, ks + KS, ...; the waves meet in LDS for the
+    // row max, the exp sum and the context sums, and wave 0 writes the context
+    constexpr int NT = (NKT + KS - 1) / KS;   // key tiles per wave
+    const int ks = KS > 1 ? tid >> 6 : 0;
+    auto tg = [&](int i) __attribute__((always_inline)) { return ks + KS * i; };   // tile of slot i
+    uint32_t pk[NT][8];   // packed int16 scores
     if constexpr (ahead) load_k(g0, kr[0]);
 #pragma unroll
-    for (int t = 0; t < NKT; ++t) {
-      if (t < ntile) {
+    for (int t = 0; t < NT; ++t) {
+      if (tg(t) < ntile) {
         if constexpr (ahead) {
           if (t + 1 < ntile) load_k(g0 + t + 1, kr[(t + 1) & 1]);
           else load_v(g0, vf[0]);   // the first V tile, while the last scores and the sums run
         } else {
-          load_k(g0 + t, kr[0]);
+          load_k(g0 + tg(t), kr[0]);
         }
         int32_t sc[16];
-        scores(g0 + t, kr[ahead ? t & 1 : 0], sc, Full{});
+        scores(g0 + tg(t), kr[ahead ? t & 1 : 0], sc, Full{});
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           pk[t][i] = ((uint32_t)sc[2 * i] & 0xFFFFu) | ((uint32_t)sc[2 * i + 1] << 16);
@@ -1415,6 +1426,12 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
       }
     }
     rowmax = max(rowmax, __shfl_xor(rowmax, 32));
+    if constexpr (KS > 1) {
+      if (h == 0) xmax[ks][c] = rowmax;
+      __syncthreads();
+#pragma unroll
+      for (int k = 0; k < KS; ++k) rowmax = max(rowmax, xmax[k][c]);
+    }
     // The packed scores become packed byte offsets 4 min(rowmax - s, 1537) into the exp table
     // (rowmax - s lies in [0, 65535], so 16-bit lanes hold it and the shifted offset), 3 packed
     // operations per 2 keys, once for both lookup passes.  A masked key holds score kMasked, which
@@ -1425,15 +1442,15 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
     const bool clean = __all(rowmax > kMasked + kDMax);
     const u16x2 rm2 = (u16x2)(unsigned short)rowmax, cap2 = (u16x2)(unsigned short)(kDMax + 1);
 #pragma unroll
-    for (int t = 0; t < NKT; ++t)
-      if (t < ntile) {
-        if (!clean && (32 * (g0 + t) < s0 || 32 * (g0 + t) + 31 > q0)) {
+    for (int t = 0; t < NT; ++t)
+      if (tg(t) < ntile) {
+        if (!clean && (32 * (g0 + tg(t)) < s0 || 32 * (g0 + tg(t)) + 31 > q0)) {
 #pragma unroll
           for (int i = 0; i < 8; ++i) {
             uint32_t off[2];
 #pragma unroll
             for (int b = 0; b < 2; ++b) {
-              const int j = 2 * i + b, key = 32 * (g0 + t) + 16 * h + j;
+              const int j = 2 * i + b, key = 32 * (g0 + tg(t)) + 16 * h + j;
               const int32_t sj = b ? (int32_t)pk[t][i] >> 16 : (int32_t)(pk[t][i] << 16) >> 16;
               off[b] = 4u * (uint32_t)(key < s0 || key > qi ? kDMax + 1 : min(rowmax - sj, kDMax + 1));
             }
@@ -1455,8 +1472,8 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
     // Z: e <= 2^30, so sums of three fit uint32
     uint64_t Z = 0;
 #pragma unroll
-    for (int t = 0; t < NKT; ++t)
-      if (t < ntile) {
+    for (int t = 0; t < NT; ++t)
+      if (tg(t) < ntile) {
         uint32_t ev[16];
 #pragma unroll
         for (int j = 0; j < 16; ++j) ev[j] = ex(t, j);
@@ -1464,20 +1481,68 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
         for (int j = 0; j < 15; j += 3) Z += ev[j] + ev[j + 1] + ev[j + 2];
         Z += ev[15];
       }
-    set_z((int64_t)Z);
+    if constexpr (KS > 1) {
+      Z += __shfl_xor(Z, 32);
+      if (h == 0) xz[ks][c] = Z;
+      __syncthreads();
+      Z = 0;
 #pragma unroll
-    for (int t = 0; t < NKT; ++t)
-      if (t < ntile) {
+      for (int k = 0; k < KS; ++k) Z += xz[k][c];
+      set_z((int64_t)Z, false);
+    } else {
+      set_z((int64_t)Z, true);
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+      if (tg(t) < ntile) {
         if constexpr (ahead) {
           if (t + 1 < ntile) load_v(g0 + t + 1, vf[(t + 1) & 1]);
         } else {
-          load_v(g0 + t, vf[0]);
+          load_v(g0 + tg(t), vf[0]);
         }
         int32_t ev[16];
 #pragma unroll
         for (int j = 0; j < 16; ++j) ev[j] = ex(t, j);
         pv(vf[ahead ? t & 1 : 0], ev);
       }
+    if constexpr (KS > 1) {
+      // context sums: wave 0's partial sums seed LDS, the other waves add theirs (exact int32
+      // sums of the single-wave totals), wave 0 reads the totals back
+      if (ks == 0) {
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+          for (int j = 0; j < 16; ++j) {
+            xc[(0 * 2 + dt) * 16 + j][lane] = C16[dt][j];
+            xc[(1 * 2 + dt) * 16 + j][lane] = C8[dt][j];
+            xc[(2 * 2 + dt) * 16 + j][lane] = C0[dt][j];
+          }
+        xsp[lane] = SP;
+      }
+      __syncthreads();
+      if (ks != 0) {
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+          for (int j = 0; j < 16; ++j) {
+            atomicAdd(&xc[(0 * 2 + dt) * 16 + j][lane], C16[dt][j]);
+            atomicAdd(&xc[(1 * 2 + dt) * 16 + j][lane], C8[dt][j]);
+            atomicAdd(&xc[(2 * 2 + dt) * 16 + j][lane], C0[dt][j]);
+          }
+        atomicAdd(&xsp[lane], SP);
+      }
+      __syncthreads();
+      if (ks != 0) return;
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          C16[dt][j] = xc[(0 * 2 + dt) * 16 + j][lane];
+          C8[dt][j] = xc[(1 * 2 + dt) * 16 + j][lane];
+          C0[dt][j] = xc[(2 * 2 + dt) * 16 + j][lane];
+        }
+      SP = xsp[lane];
+    }
   } else {
     recompute_passes();
   }
@@ -1870,12 +1935,26 @@ hipError_t attention(const AttnArgs& a, hipStream_t s) {
   // head for the longer rows, whose passes recompute the scores
   const int nqt = (a.max_T + 31) / 32 - (a.q_first >> 5);
   const dim3 grid((unsigned)(((size_t)nqt * a.B * kNH + 3) / 4)), block(256), grid1(a.B, kNH, nqt), block1(64);
+  // with fewer than 2048 (sequence, head, query tile) tasks (a few sequences: fewer than two waves per
+  // SIMD) each task's key tiles are split over the 4 waves of its workgroup, which shortens the
+  // serial chain of the longest task
+  const bool split = (size_t)nqt * a.B * kNH < 2048;
   if (a.max_kt <= 5) {
-    if (a.bits_c == 16) hipLaunchKernelGGL((attn_kernel<2, 5, 4>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((attn_kernel<4, 5, 4>), grid, block, 0, s, a);
+    if (split) {
+      if (a.bits_c == 16) hipLaunchKernelGGL((attn_kernel<2, 5, 4, 4>), grid1, block, 0, s, a);
+      else hipLaunchKernelGGL((attn_kernel<4, 5, 4, 4>), grid1, block, 0, s, a);
+    } else {
+      if (a.bits_c == 16) hipLaunchKernelGGL((attn_kernel<2, 5, 4>), grid, block, 0, s, a);
+      else hipLaunchKernelGGL((attn_kernel<4, 5, 4>), grid, block, 0, s, a);
+    }
   } else if (a.max_kt <= 8) {
-    if (a.bits_c == 16) hipLaunchKernelGGL((attn_kernel<2, 8, 4>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((attn_kernel<4, 8, 4>), grid, block, 0, s, a);
+    if (split) {
+      if (a.bits_c == 16) hipLaunchKernelGGL((attn_kernel<2, 8, 4, 4>), grid1, block, 0, s, a);
+      else hipLaunchKernelGGL((attn_kernel<4, 8, 4, 4>), grid1, block, 0, s, a);
+    } else {
+      if (a.bits_c == 16) hipLaunchKernelGGL((attn_kernel<2, 8, 4>), grid, block, 0, s, a);
+      else hipLaunchKernelGGL((attn_kernel<4, 8, 4>), grid, block, 0, s, a);
+    }
   } else {
     if (a.bits_c == 16) hipLaunchKernelGGL((attn_kernel<2, 0, 1>), grid1, block1, 0, s, a);
     else hipLaunchKernelGGL((attn_kernel<4, 0, 1>), grid1, block1, 0, s, a);

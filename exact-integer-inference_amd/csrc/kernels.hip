@@ -1023,7 +1023,7 @@ __device__ __forceinline__ int32_t sum16x8(u32x4 d, int32_t s = 0) {   // s + th
 template <int OB, int NKT, int WPG, int KS = 1>
 __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) void attn_kernel(AttnArgs a) {
   static_assert(WPG == 1 || WPG == 4, "one wave per workgroup, or 4 waves");
-  static_assert(KS == 1 || (KS == WPG && NKT > 0), "key tiles split over the waves of one task");
+  static_assert(KS == 1 || KS == WPG, "key tiles split over the waves of one task");
   __shared__ int32_t etab[kDMax + 2];                              // exp table, etab[1537] = 0
   __shared__ __attribute__((aligned(16))) int32_t sklw[WPG][32];   // per wave: 128 * sum_d k per key
   __shared__ __attribute__((aligned(16))) v4i qxw[NKT == 0 ? WPG : 1][2][64];   // per wave: qx digits
@@ -1333,25 +1333,96 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
   constexpr bool ahead = NKT > 0 && NKT <= 5 && KS == 1;
   KRows kr[ahead ? 2 : 1];
   VFrag vf[ahead ? 2 : 1];
-  // every pass recomputes the scores; the exp lookups test keys only in waves with a row max
-  // near -32768 (see the register-resident passes below)
-  // The row-max and exp-sum passes load the K rows of tile t + 1 while tile t computes (two tiles
-  // per iteration, so the buffer of each is a compile-time choice); the P.V pass, whose registers
-  // hold the context sums, loads each tile's K and V at its start.
+  // KS > 1: wave ks of the task takes key tiles ks, ks + KS, ... (tile tg(i) of its slot i, nloc
+  // slots); the waves meet in LDS for the row max, the exp sum and the context sums, and wave 0
+  // writes the context
+  const int ks = KS > 1 ? tid >> 6 : 0;
+  const int nloc = KS == 1 ? ntile : ks < ntile ? (ntile - ks + KS - 1) / KS : 0;
+  auto tg = [&](int i) __attribute__((always_inline)) { return KS == 1 ? i : ks + KS * i; };
+  auto combine_max = [&](int32_t m) __attribute__((always_inline)) {   // m: both lane halves' max
+    if constexpr (KS > 1) {
+      if (h == 0) xmax[ks][c] = m;
+      __syncthreads();
+#pragma unroll
+      for (int k = 0; k < KS; ++k) m = max(m, xmax[k][c]);
+    }
+    return m;
+  };
+  auto combine_z = [&](uint64_t Z) __attribute__((always_inline)) {   // the exp sum setup
+    if constexpr (KS > 1) {
+      Z += __shfl_xor(Z, 32);
+      if (h == 0) xz[ks][c] = Z;
+      __syncthreads();
+      Z = 0;
+#pragma unroll
+      for (int k = 0; k < KS; ++k) Z += xz[k][c];
+      set_z((int64_t)Z, false);
+    } else {
+      set_z((int64_t)Z, true);
+    }
+  };
+  // context sums: wave 0's partial sums seed LDS, the other waves add theirs (exact int32 sums of
+  // the single-wave totals) and leave, wave 0 reads the totals back; returns false in the waves
+  // that leave
+  auto combine_ctx = [&]() __attribute__((always_inline)) -> bool {
+    if constexpr (KS > 1) {
+      if (ks == 0) {
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+          for (int j = 0; j < 16; ++j) {
+            xc[(0 * 2 + dt) * 16 + j][lane] = C16[dt][j];
+            xc[(1 * 2 + dt) * 16 + j][lane] = C8[dt][j];
+            xc[(2 * 2 + dt) * 16 + j][lane] = C0[dt][j];
+          }
+        xsp[lane] = SP;
+      }
+      __syncthreads();
+      if (ks != 0) {
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+          for (int j = 0; j < 16; ++j) {
+            atomicAdd(&xc[(0 * 2 + dt) * 16 + j][lane], C16[dt][j]);
+            atomicAdd(&xc[(1 * 2 + dt) * 16 + j][lane], C8[dt][j]);
+            atomicAdd(&xc[(2 * 2 + dt) * 16 + j][lane], C0[dt][j]);
+          }
+        atomicAdd(&xsp[lane], SP);
+      }
+      __syncthreads();
+      if (ks != 0) return false;
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          C16[dt][j] = xc[(0 * 2 + dt) * 16 + j][lane];
+          C8[dt][j] = xc[(1 * 2 + dt) * 16 + j][lane];
+          C0[dt][j] = xc[(2 * 2 + dt) * 16 + j][lane];
+        }
+      SP = xsp[lane];
+    }
+    return true;
+  };
+
+  // Long rows: every pass recomputes the scores; the exp lookups test keys only in waves with a
+  // row max near -32768 (see the register-resident passes below).  The row-max and exp-sum passes
+  // load the K rows of the wave's next tile while the current one computes (two slots per
+  // iteration, so the buffer of each is a compile-time choice); the P.V pass, whose registers hold
+  // the context sums, loads each tile's K and V at its start.
   auto recompute_passes = [&]() __attribute__((always_inline)) {
     KRows kb[2];
     auto max_pass = [&](auto RAW) __attribute__((always_inline)) {
       int32_t m = INT32_MIN;
-      load_k(g0, kb[0]);
+      if (KS == 1 || nloc > 0) load_k(g0 + tg(0), kb[0]);
 #pragma unroll 1
-      for (int t0 = 0; t0 < ntile; t0 += 2) {
+      for (int t0 = 0; t0 < nloc; t0 += 2) {
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
           const int t = t0 + u;
-          if (t < ntile) {
-            if (t + 1 < ntile) load_k(g0 + t + 1, kb[u ^ 1]);
+          if (t < nloc) {
+            if (t + 1 < nloc) load_k(g0 + tg(t + 1), kb[u ^ 1]);
             int32_t sc[16];
-            scores(g0 + t, kb[u], sc, RAW);
+            scores(g0 + tg(t), kb[u], sc, RAW);
 #pragma unroll
             for (int j = 0; j < 16; ++j) m = max(m, sc[j]);
           }
@@ -1361,36 +1432,36 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
     };
     if (sh >= 16) rowmax = min(max(max_pass(Raw{}) >> (sh - 16), -32768), 32767);
     else rowmax = max_pass(Full{});
-    rowmax = max(rowmax, __shfl_xor(rowmax, 32));
+    rowmax = combine_max(max(rowmax, __shfl_xor(rowmax, 32)));
     auto passes = [&](auto CLEAN) __attribute__((always_inline)) {
       auto ex = [&](int t, int j, int32_t s) __attribute__((always_inline)) -> uint32_t {
         if constexpr (decltype(CLEAN)::value) return (uint32_t)etab[min(rowmax - s, kDMax + 1)];
-        else return (uint32_t)expo(g0 + t, j, s, rowmax);
+        else return (uint32_t)expo(g0 + tg(t), j, s, rowmax);
       };
       uint64_t Z = 0;   // e <= 2^30: sums of three fit uint32
-      load_k(g0, kb[0]);
+      if (KS == 1 || nloc > 0) load_k(g0 + tg(0), kb[0]);
 #pragma unroll 1
-      for (int t0 = 0; t0 < ntile; t0 += 2) {
+      for (int t0 = 0; t0 < nloc; t0 += 2) {
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
           const int t = t0 + u;
-          if (t < ntile) {
-            if (t + 1 < ntile) load_k(g0 + t + 1, kb[u ^ 1]);
+          if (t < nloc) {
+            if (t + 1 < nloc) load_k(g0 + tg(t + 1), kb[u ^ 1]);
             int32_t sc[16];
-            scores(g0 + t, kb[u], sc, Full{});
+            scores(g0 + tg(t), kb[u], sc, Full{});
 #pragma unroll
             for (int j = 0; j < 15; j += 3) Z += ex(t, j, sc[j]) + ex(t, j + 1, sc[j + 1]) + ex(t, j + 2, sc[j + 2]);
             Z += ex(t, 15, sc[15]);
           }
         }
       }
-      set_z((int64_t)Z);
+      combine_z(Z);
 #pragma unroll 1
-      for (int t = 0; t < ntile; ++t) {
+      for (int t = 0; t < nloc; ++t) {
         int32_t sc[16];
-        load_k(g0 + t, kr[0]);
-        load_v(g0 + t, vf[0]);
-        scores(g0 + t, kr[0], sc, Full{});
+        load_k(g0 + tg(t), kr[0]);
+        load_v(g0 + tg(t), vf[0]);
+        scores(g0 + tg(t), kr[0], sc, Full{});
 #pragma unroll
         for (int j = 0; j < 16; ++j) sc[j] = (int32_t)ex(t, j, sc[j]);
         pv(vf[0], sc);
@@ -1400,11 +1471,7 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
     else passes(std::false_type{});
   };
   if constexpr (NKT > 0) {
-    // KS > 1: wave ks of the task takes key tiles ks, ks + KS, ...; the waves meet in LDS for the
-    // row max, the exp sum and the context sums, and wave 0 writes the context
     constexpr int NT = (NKT + KS - 1) / KS;   // key tiles per wave
-    const int ks = KS > 1 ? tid >> 6 : 0;
-    auto tg = [&](int i) __attribute__((always_inline)) { return ks + KS * i; };   // tile of slot i
     uint32_t pk[NT][8];   // packed int16 scores
     if constexpr (ahead) load_k(g0, kr[0]);
 #pragma unroll
@@ -1425,13 +1492,7 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
         }
       }
     }
-    rowmax = max(rowmax, __shfl_xor(rowmax, 32));
-    if constexpr (KS > 1) {
-      if (h == 0) xmax[ks][c] = rowmax;
-      __syncthreads();
-#pragma unroll
-      for (int k = 0; k < KS; ++k) rowmax = max(rowmax, xmax[k][c]);
-    }
+    rowmax = combine_max(max(rowmax, __shfl_xor(rowmax, 32)));
     // The packed scores become packed byte offsets 4 min(rowmax - s, 1537) into the exp table
     // (rowmax - s lies in [0, 65535], so 16-bit lanes hold it and the shifted offset), 3 packed
     // operations per 2 keys, once for both lookup passes.  A masked key holds score kMasked, which
@@ -1481,17 +1542,7 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
         for (int j = 0; j < 15; j += 3) Z += ev[j] + ev[j + 1] + ev[j + 2];
         Z += ev[15];
       }
-    if constexpr (KS > 1) {
-      Z += __shfl_xor(Z, 32);
-      if (h == 0) xz[ks][c] = Z;
-      __syncthreads();
-      Z = 0;
-#pragma unroll
-      for (int k = 0; k < KS; ++k) Z += xz[k][c];
-      set_z((int64_t)Z, false);
-    } else {
-      set_z((int64_t)Z, true);
-    }
+    combine_z(Z);
 #pragma unroll
     for (int t = 0; t < NT; ++t)
       if (tg(t) < ntile) {
@@ -1505,46 +1556,10 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
         for (int j = 0; j < 16; ++j) ev[j] = ex(t, j);
         pv(vf[ahead ? t & 1 : 0], ev);
       }
-    if constexpr (KS > 1) {
-      // context sums: wave 0's partial sums seed LDS, the other waves add theirs (exact int32
-      // sums of the single-wave totals), wave 0 reads the totals back
-      if (ks == 0) {
-#pragma unroll
-        for (int dt = 0; dt < 2; ++dt)
-#pragma unroll
-          for (int j = 0; j < 16; ++j) {
-            xc[(0 * 2 + dt) * 16 + j][lane] = C16[dt][j];
-            xc[(1 * 2 + dt) * 16 + j][lane] = C8[dt][j];
-            xc[(2 * 2 + dt) * 16 + j][lane] = C0[dt][j];
-          }
-        xsp[lane] = SP;
-      }
-      __syncthreads();
-      if (ks != 0) {
-#pragma unroll
-        for (int dt = 0; dt < 2; ++dt)
-#pragma unroll
-          for (int j = 0; j < 16; ++j) {
-            atomicAdd(&xc[(0 * 2 + dt) * 16 + j][lane], C16[dt][j]);
-            atomicAdd(&xc[(1 * 2 + dt) * 16 + j][lane], C8[dt][j]);
-            atomicAdd(&xc[(2 * 2 + dt) * 16 + j][lane], C0[dt][j]);
-          }
-        atomicAdd(&xsp[lane], SP);
-      }
-      __syncthreads();
-      if (ks != 0) return;
-#pragma unroll
-      for (int dt = 0; dt < 2; ++dt)
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          C16[dt][j] = xc[(0 * 2 + dt) * 16 + j][lane];
-          C8[dt][j] = xc[(1 * 2 + dt) * 16 + j][lane];
-          C0[dt][j] = xc[(2 * 2 + dt) * 16 + j][lane];
-        }
-      SP = xsp[lane];
-    }
+    if (!combine_ctx()) return;
   } else {
     recompute_passes();
+    if (!combine_ctx()) return;
   }
   SP += __shfl_xor(SP, 32);
 
@@ -1955,6 +1970,9 @@ hipError_t attention(const AttnArgs& a, hipStream_t s) {
       if (a.bits_c == 16) hipLaunchKernelGGL((attn_kernel<2, 8, 4>), grid, block, 0, s, a);
       else hipLaunchKernelGGL((attn_kernel<4, 8, 4>), grid, block, 0, s, a);
     }
+  } else if (split) {
+    if (a.bits_c == 16) hipLaunchKernelGGL((attn_kernel<2, 0, 4, 4>), grid1, block, 0, s, a);
+    else hipLaunchKernelGGL((attn_kernel<4, 0, 4, 4>), grid1, block, 0, s, a);
   } else {
     if (a.bits_c == 16) hipLaunchKernelGGL((attn_kernel<2, 0, 1>), grid1, block1, 0, s, a);
     else hipLaunchKernelGGL((attn_kernel<4, 0, 1>), grid1, block1, 0, s, a);

@@ -572,6 +572,21 @@ __global__ __launch_bounds__(256, SHAPE == kShapeSkinny || SHAPE == kShapeSkinny
           wf[i][tn] = *(const v4i*)(g.W + w_frag(nb32, kslices, sl, lane));
         }
       }
+    // wave 0 reads the epilogue's per-column coefficients (and the residual row, or the positions)
+    // while the operands load, so the epilogue's own reads of them hit the CU's cache instead of
+    // adding a memory round trip after the reduction
+    uint32_t touch = 0;
+    if (wave == 0) {
+      const int n = min(nb * C::BN + fc, g.N - 1), n2 = min(n + 32, g.N - 1);
+      if constexpr (AW == 2 && EPI != EPI_I64) {
+        touch = (uint32_t)__double_as_longlong(g.coef[n].x) ^ (uint32_t)__double_as_longlong(g.coef[n2].y);
+      } else if constexpr (EPI != EPI_I64) {
+        touch = (uint32_t)(g.mult[n] ^ g.shift[n] ^ g.wsum[n]);
+      }
+      const int mr = min(mb * C::BM + 4 * fh, g.M - 1);
+      if constexpr (EPI == EPI_RESID) touch ^= (uint32_t)((const int32_t*)g.out)[(size_t)mr * g.N + n];
+      if constexpr (EPI == EPI_QKV) touch ^= (uint32_t)g.pos[mr];
+    }
 #pragma unroll
     for (int i = 0; i < NSW; ++i)
       if (i < cnt) {
@@ -580,6 +595,7 @@ __global__ __launch_bounds__(256, SHAPE == kShapeSkinny || SHAPE == kShapeSkinny
 #pragma unroll
           for (int tn = 0; tn < C::TN; ++tn) acc[0][tn][l] = mfma32(af[i][l], wf[i][tn], acc[0][tn][l]);
       }
+    __asm__ volatile("" ::"v"(touch));   // keeps the reads
     // partial sums of waves 1..3 -> LDS as 16-byte groups [wave - 1][tn][l][e / 4][lane][e % 4];
     // wave 0 adds them (each partial and the total are limb sums over part of K, below 2^31) and runs
     // the epilogue

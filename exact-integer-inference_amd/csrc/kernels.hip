@@ -572,9 +572,9 @@ __global__ __launch_bounds__(256, SHAPE == kShapeSkinny || SHAPE == kShapeSkinny
           wf[i][tn] = *(const v4i*)(g.W + w_frag(nb32, kslices, sl, lane));
         }
       }
-    // wave 0 reads the epilogue's per-column coefficients (and the residual row, or the positions)
-    // while the operands load, so the epilogue's own reads of them hit the CU's cache instead of
-    // adding a memory round trip after the reduction
+    // wave 0 reads the epilogue's per-column coefficients and, lane c for tile row c, the residual
+    // row or the position and its RoPE rows while the operands load, so the epilogue's own reads of
+    // them hit the CU's cache instead of adding memory round trips after the reduction
     uint32_t touch = 0;
     if (wave == 0) {
       const int n = min(nb * C::BN + fc, g.N - 1), n2 = min(n + 32, g.N - 1);
@@ -583,9 +583,12 @@ __global__ __launch_bounds__(256, SHAPE == kShapeSkinny || SHAPE == kShapeSkinny
       } else if constexpr (EPI != EPI_I64) {
         touch = (uint32_t)(g.mult[n] ^ g.shift[n] ^ g.wsum[n]);
       }
-      const int mr = min(mb * C::BM + 4 * fh, g.M - 1);
-      if constexpr (EPI == EPI_RESID) touch ^= (uint32_t)((const int32_t*)g.out)[(size_t)mr * g.N + n];
-      if constexpr (EPI == EPI_QKV) touch ^= (uint32_t)g.pos[mr];
+      const int mr = min(mb * C::BM + fc, g.M - 1);
+      if constexpr (EPI == EPI_RESID) touch ^= (uint32_t)((const int32_t*)g.out)[(size_t)mr * g.N + nb * C::BN];
+      if constexpr (EPI == EPI_QKV) {
+        const int ps = g.pos[mr];
+        touch ^= (uint32_t)(g.cosT[ps * 32] ^ g.sinT[ps * 32]);
+      }
     }
 #pragma unroll
     for (int i = 0; i < NSW; ++i)

@@ -1619,23 +1619,25 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
 // Decoding attention: one new query per sequence (the last of its kv_len cached rows) against
 // all of them, python/intref.py:227-254 with T = kv_len and only the last query row.  Workgroup =
 // one sequence and one kv group: NW waves per query head 3 kvg + hq (NW = 4 for few sequences,
-// where the latency of one workgroup is the step's; 1 when the sequences fill the GPU); the keys
-// go in 64-key chunks, chunk c to wave c % NW of each head.  Lane j of a wave scores key 64 c + j (64 int16
-// products summed exactly in int64; the SAT16 score kept in LDS) and, once the row max and the exp
-// sum Z are known (wave reductions, then the head's 4 waves through LDS), forms its key's
-// probability P = floor((e 65536 + floor(Z / 2)) / Z) from a float64 quotient and an exact
-// remainder correction; the lanes then, one per head dimension, sum P v over the chunk in int64
-// with each P taken from its lane by v_readlane, and the head's 4 partial sums meet in LDS.  A
-// wave's first value chunk is loaded before the reductions, so its latency hides behind them.
-// No key is masked: every cached key precedes the query.
+// where the latency of one workgroup is the step's; 1 when the sequences fill the GPU).  The scores
+// of all 3 heads come from MFMAs over 32-key tiles shared out among all the workgroup's waves (the
+// 3 queries as B-operand columns) and go to LDS as SAT16 values with each wave's per-head max; then
+// the keys go in 64-key chunks, chunk c to wave c % NW of each head: once the row max and the exp
+// sum Z are known (through LDS and wave reductions), lane j forms key 64 c + j's probability
+// P = floor((e 65536 + floor(Z / 2)) / Z) from a float64 quotient and an exact remainder
+// correction; the lanes then, one per head dimension, sum P v over the chunk in int64 with each P
+// taken from its lane by v_readlane, and the head's NW partial sums meet in LDS.  A wave's first
+// value chunk is loaded before the reductions, so its latency hides behind them.  No key is
+// masked: every cached key precedes the query.
 // scores of 3 heads x kDecodeMaxKeys keys: 48 KB of LDS (kernels.h)
-// LDS: exp table [1537] + 3 pad ints (the end stays 16-byte aligned), the row maxima [3 NW] in an
-// even count of ints (so the int64 arrays after them are 8-byte aligned for every NW), the exp sums
-// [3 NW] and partial context sums [3 NW][64] as int64, the scores of 3 heads as int16
-__host__ __device__ inline int attn_decode_nmax(int NW) { return (3 * NW + 1) & ~1; }
+// LDS: exp table [1537] + 3 pad ints (the end stays 16-byte aligned), each wave's max of each head
+// [3 NW][4] (an even count of ints, so the int64 arrays after them are 8-byte aligned), the exp
+// sums [3 NW] and partial context sums [3 NW][64] as int64, the scores of 3 heads as int16, and per
+// wave the 32 per-key sums of k of its current tile
+__host__ __device__ inline int attn_decode_nmax(int NW) { return 12 * NW; }
 __host__ __device__ inline size_t attn_decode_lds(int L, int NW) {
   return (size_t)(kDMax + 1 + 3) * 4 + (size_t)attn_decode_nmax(NW) * 4 + (size_t)3 * NW * (8 + 64 * 8) +
-         (size_t)3 * ((L + 63) & ~63) * 2;
+         (size_t)3 * ((L + 63) & ~63) * 2 + (size_t)3 * NW * 32 * 4;
 }
 
 template <int OB, int NW>
@@ -1645,41 +1647,83 @@ __global__ __launch_bounds__(64 * 3 * NW) void attn_decode_kernel(AttnArgs a) {
   const int seq = blockIdx.x, kvg = blockIdx.y, hh = 3 * kvg + hq;
   const int L = a.kv_len, Lp = (L + 63) & ~63;
   int32_t* etab = dsm;                                          // [1537] (+3 pad)
-  int32_t* smax = dsm + kDMax + 1 + 3;                          // [3 NW], padded to an even count
+  int32_t* smax = dsm + kDMax + 1 + 3;                          // [3 NW][4]: each wave's max of each head
   int64_t* sz = (int64_t*)(smax + attn_decode_nmax(NW));        // [3 NW]
   int64_t* spart = sz + 3 * NW;                                 // [12][64]
-  int16_t* sc = (int16_t*)(spart + 3 * NW * 64) + (size_t)hq * Lp;
   for (int i = tid; i <= kDMax; i += 64 * 3 * NW) etab[i] = a.exp_tab[i];
   const int16_t* base = a.qkv + (size_t)a.seq_off[seq] * kQKVN;   // key 0 of the sequence
-  const int4* q4 = (const int4*)(base + (size_t)(L - 1) * kQKVN + hh * 64);
-  int4 q[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) q[i] = q4[i];
+  int16_t* const sc_all = (int16_t*)(spart + 3 * NW * 64);      // [3][Lp]
+  int32_t* const skl = (int32_t*)(sc_all + 3 * Lp) + 32 * w;     // per wave: 128 sum_d k per key
 
-  // scores of this wave's chunks and their max (a key past L re-reads key L - 1, not stored)
-  int32_t mx = INT32_MIN;
-  for (int c = kw; 64 * c < L; c += NW) {
-    const int j = 64 * c + lane;
-    const int4* k4 = (const int4*)(base + (size_t)min(j, L - 1) * kQKVN + kD + kvg * 64);
-    int4 kk[8];
+  // Scores of the 3 heads on v_mfma_i32_32x32x32_i8 with attn_kernel's operand forms and key order
+  // (S^T = K . Q^T, k = 256 KH + KL' + 128 and q likewise, the per-key sums of k through LDS): the
+  // B operand's columns 0..2 carry the heads' queries (the other columns repeat head 2 and are
+  // dropped), and wave w of the 3 NW takes the 32-key tiles w, w + 3 NW, ...; lanes c < 3 of each
+  // half end with head c's scores of keys 16 h + j, which go to LDS with the head's running max.
+  const int c = lane & 31, h = lane >> 5, pic = attn_key_perm(c), sh = a.shift_s;
+  v4i ql[2], qh[2];
+  int32_t cq;
+  {
+    const int16_t* qp = base + (size_t)(L - 1) * kQKVN + (3 * kvg + min(c, 2)) * 64 + 16 * h;
+    int32_t sum = 0;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) kk[i] = k4[i];
-    int64_t acc = 0;
+    for (int s2 = 0; s2 < 2; ++s2) {
+      const u32x4 d0 = *(const u32x4*)(qp + 32 * s2), d1 = *(const u32x4*)(qp + 32 * s2 + 8);
+      ql[s2] = v4i{(int)lo_bytes16(d0[0], d0[1]), (int)lo_bytes16(d0[2], d0[3]), (int)lo_bytes16(d1[0], d1[1]),
+                   (int)lo_bytes16(d1[2], d1[3])};
+      qh[s2] = v4i{(int)hi_bytes16(d0[0], d0[1]), (int)hi_bytes16(d0[2], d0[3]), (int)hi_bytes16(d1[0], d1[1]),
+                   (int)hi_bytes16(d1[2], d1[3])};
+      sum = sum16x8(d1, sum16x8(d0, sum));
+    }
+    sum += __shfl_xor(sum, 32);
+    cq = 128 * sum - (1 << 20) + (1 << (sh - 1));   // with the rounding offset of RS(., sh)
+  }
+  int32_t mxh = INT32_MIN;
+  const int16_t* const kbase = base + kD + kvg * 64 + 16 * h;
+  for (int tt = w; 32 * tt < L; tt += 3 * NW) {
+    const int16_t* kp = kbase + (size_t)min(32 * tt + pic, L - 1) * kQKVN;   // keys past L re-read L - 1
+    v4i kl[2], kh[2];
+    int32_t ks = 0;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int32_t qw[4] = {q[i].x, q[i].y, q[i].z, q[i].w}, kw4[4] = {kk[i].x, kk[i].y, kk[i].z, kk[i].w};
+    for (int s2 = 0; s2 < 2; ++s2) {
+      const u32x4 d0 = *(const u32x4*)(kp + 32 * s2), d1 = *(const u32x4*)(kp + 32 * s2 + 8);
+      kl[s2] = v4i{(int)lo_bytes16(d0[0], d0[1]), (int)lo_bytes16(d0[2], d0[3]), (int)lo_bytes16(d1[0], d1[1]),
+                   (int)lo_bytes16(d1[2], d1[3])};
+      kh[s2] = v4i{(int)hi_bytes16(d0[0], d0[1]), (int)hi_bytes16(d0[2], d0[3]), (int)hi_bytes16(d1[0], d1[1]),
+                   (int)hi_bytes16(d1[2], d1[3])};
+      ks = sum16x8(d1, sum16x8(d0, ks));
+    }
+    ks += __shfl_xor(ks, 32);
+    skl[pic] = 128 * ks;   // lanes c and c + 32 store the same value
+    __builtin_amdgcn_wave_barrier();
+    v16i a16 = v16i{}, a8 = v16i{}, a0 = v16i{};
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        acc += (int64_t)((int32_t)(int16_t)qw[r] * (int32_t)(int16_t)kw4[r]);
-        acc += (int64_t)((qw[r] >> 16) * (kw4[r] >> 16));
+    for (int s2 = 0; s2 < 2; ++s2) {
+      a16 = mfma32(kh[s2], qh[s2], a16);
+      a8 = mfma32(kh[s2], ql[s2], a8);
+      a8 = mfma32(kl[s2], qh[s2], a8);
+      a0 = mfma32(kl[s2], ql[s2], a0);
+    }
+    const v4i* kk = (const v4i*)&skl[16 * h];
+    const v4i k4[4] = {kk[0], kk[1], kk[2], kk[3]};
+    __builtin_amdgcn_wave_barrier();
+    if (c < 3) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int32_t lo = a8[j] * 256 + a0[j] + k4[j >> 2][j & 3] + cq, wv = a16[j] + (lo >> 16);
+        const int32_t sv = sh >= 16 ? min(max(wv >> (sh - 16), -32768), 32767)
+                                    : min(max(min(max(wv, -32769), 32768) * (1 << (16 - sh)) + ((lo & 0xFFFF) >> sh), -32768), 32767);
+        const int key = 32 * tt + 16 * h + j;
+        if (key < L) {
+          sc_all[c * Lp + key] = (int16_t)sv;
+          mxh = max(mxh, sv);
+        }
       }
     }
-    const int32_t sv = (int32_t)sat(rs(acc, a.shift_s), 16);
-    if (j < L) {
-      sc[j] = (int16_t)sv;
-      mx = max(mx, sv);
-    }
   }
+  mxh = max(mxh, __shfl_xor(mxh, 32));
+  if (lane < 3) smax[4 * w + lane] = mxh;
+  int16_t* const sc = sc_all + (size_t)hq * Lp;
   // the value rows of this wave's first chunk, loaded now (rows past L re-read row L - 1)
   const int16_t* vcol = base + kD + 192 + kvg * 64 + lane;
   int32_t vv[64];
@@ -1688,13 +1732,10 @@ __global__ __launch_bounds__(64 * 3 * NW) void attn_decode_kernel(AttnArgs a) {
 #pragma unroll
     for (int jj = 0; jj < 64; ++jj) vv[jj] = vcol[(size_t)(64 * kw + min(jj, n - 1)) * kQKVN];
   }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) mx = max(mx, __shfl_xor(mx, o));
-  if (lane == 0) smax[w] = mx;
   __syncthreads();
-  mx = smax[hq * NW];
+  int32_t mx = INT32_MIN;
 #pragma unroll
-  for (int k = 1; k < NW; ++k) mx = max(mx, smax[hq * NW + k]);
+  for (int k = 0; k < 3 * NW; ++k) mx = max(mx, smax[4 * k + hq]);
   // Z = sum of the table entries of d = max - s <= 1536 (entries beyond are 0); Z >= 2^30
   int64_t Z = 0;
   for (int c = kw; 64 * c < L; c += NW) {

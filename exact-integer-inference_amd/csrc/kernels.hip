@@ -865,6 +865,26 @@ __global__ __launch_bounds__(256) void embed_kernel(const int64_t* ids, int M, c
 }
 
 // ------------------------------------------------------------------------------ rmsnorm
+// v + the value of the lane that DPP control CTRL selects, for an int64 moved as two dwords
+template <int CTRL>
+__device__ __forceinline__ int64_t dpp_add64(int64_t v) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)v, CTRL, 0xF, 0xF, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)((uint64_t)v >> 32), CTRL, 0xF, 0xF, false);
+  return v + (int64_t)(((uint64_t)hi << 32) | lo);
+}
+// sum over each group of LPR lanes (16 or 64), in every lane of the group: within 16-lane rows by
+// DPP (lane ^ 1, lane ^ 2, then the mirrored lane of the other quad of the 8 and of the other 8 of
+// the row), across rows by lane shuffles
+template <int LPR>
+__device__ __forceinline__ int64_t group_sum64(int64_t v) {
+  v = dpp_add64<0xB1>(v);    // quad_perm [1, 0, 3, 2]
+  v = dpp_add64<0x4E>(v);    // quad_perm [2, 3, 0, 1]
+  v = dpp_add64<0x141>(v);   // row_half_mirror
+  v = dpp_add64<0x140>(v);   // row_mirror
+  if constexpr (LPR > 16) v += __shfl_xor(v, 16);
+  if constexpr (LPR > 32) v += __shfl_xor(v, 32);
+  return v;
+}
 // LPR lanes per row: 16 (4 rows per wave, for many rows) or 64 (a wave per row: a quarter of the
 // serial work per lane, for the few rows of a decoding step).  Lane c of a row holds the VW = 64 /
 // LPR columns 64 k + VW c .. + VW - 1, k = 0..8, so loads are 4 VW bytes, the limb bytes of a
@@ -909,10 +929,9 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const int32_t* x, int M, c
       A += (int64_t)hi * hi; B += (int64_t)hi * lo; Cs += (int64_t)lo * lo;
       if constexpr (!WIDE) g3[k][r] *= 3;
     }
-#pragma unroll
-  for (int o = LPR / 2; o > 0; o >>= 1) {
-    A += __shfl_xor(A, o); B += __shfl_xor(B, o); Cs += __shfl_xor(Cs, o);
-  }
+  A = group_sum64<LPR>(A);
+  B = group_sum64<LPR>(B);
+  Cs = group_sum64<LPR>(Cs);
   const int32_t U = (int32_t)norm_U(norm_total(A, B, Cs));   // < 2^29
   if (row >= M) return;
   if (u_out && c == 0) u_out[row] = U;

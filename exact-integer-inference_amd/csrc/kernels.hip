@@ -1764,8 +1764,7 @@ __global__ __launch_bounds__(64 * 3 * NW) void attn_decode_kernel(AttnArgs a) {
       Z += d <= kDMax ? etab[d] : 0;
     }
   }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) Z += __shfl_xor(Z, o);
+  Z = group_sum64<64>(Z);
   if (lane == 0) sz[w] = Z;
   __syncthreads();
   Z = 0;

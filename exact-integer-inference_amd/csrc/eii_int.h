@@ -78,11 +78,16 @@ EII_HD bool norm_fits(uint64_t u, u128 Tt) {
 }
 
 // The float64 estimate is within one of U (see above), so U is u - 1, u or u + 1 for
-// u = floor(estimate); the loops also cover any larger miss.
+// u = floor(estimate); the loops also cover any larger miss.  Below 2^31 the estimate's absolute
+// error is under 2^-17 (relative error below 2^-48), so when its fractional part lies more than
+// 2^-16 from 0 and from 1, no integer separates it from 2^40 / sqrt(Tt) and its floor is U without
+// the exact tests (which then only run for estimates next to an integer).
 EII_HD int64_t norm_U(u128 Tt) {
   const double td = (double)(uint64_t)(Tt >> 64) * 18446744073709551616.0 + (double)(uint64_t)Tt;
   double ue = 1099511627776.0 / sqrt(td);           // 2^40 / sqrt(Tt)
   if (ue > 2147483647.0) ue = 2147483647.0;
+  const double fl = floor(ue), fr = ue - fl;
+  if (fr > 0x1p-16 && fr < 1.0 - 0x1p-16) return (int64_t)fl;
   uint64_t u = (uint64_t)ue;
   for (int it = 0; it < 64 && u > 0 && !norm_fits(u, Tt); ++it) --u;
   for (int it = 0; it < 64 && norm_fits(u + 1, Tt); ++it) ++u;

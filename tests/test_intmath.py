@@ -66,6 +66,18 @@ def test_norm_U(hc):
         assert hc.eii_host_norm_U(A, B, Cc) == U, x[:4]
 
 
+def test_norm_U_many_sums(hc):
+    # 20000 row sums S over all magnitudes (Tt from EPS up to 2^73): the float64 estimate's floor,
+    # taken directly when its fractional part is far from 0 and 1, and the exact tests otherwise
+    rng = np.random.default_rng(5)
+    for _ in range(20000):
+        S = int(rng.integers(0, 2 ** 62)) >> int(rng.integers(0, 62))
+        S = S * (1 << int(rng.integers(0, 12)))
+        A, rem = divmod(S, 1 << 32)
+        want = math.isqrt((1 << 80) // (S + EPS_S))
+        assert hc.eii_host_norm_U(A, 0, rem) == want, S
+
+
 def test_norm_U_boundaries_direct(hc):
     # Tt = S + EPS exactly at u^2 * Tt == 2^80 and one either side, with S given by A,B,C = (0,0,S)
     for u in (11, 64, 4096, 2 ** 20, 2 ** 25):

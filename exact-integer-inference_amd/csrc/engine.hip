@@ -98,6 +98,7 @@ struct eii_model {
   void* h = nullptr;               // [M, 576] up to int32
   int16_t* qkv = nullptr;          // [M, 960]
   uint8_t* vt = nullptr;           // V^T limb planes (kernels.h vt_bytes)
+  uint8_t* kpl = nullptr;          // k limb planes of long-row attention (kernels.h attn_kpl_bytes)
   void* ctx = nullptr;             // [M, 576] up to int32
   int16_t* gu = nullptr;           // [M, 3072]
   void* gated = nullptr;           // [M, 1536] up to int32
@@ -454,9 +455,9 @@ extern "C" int eii_model_load(const char* path, int device, eii_model** out) {
 }
 
 static void free_ws(eii_model* m) {
-  void* ps[] = {m->x, m->h, m->qkv, m->vt, m->ctx, m->gu, m->gated, m->pos};
+  void* ps[] = {m->x, m->h, m->qkv, m->vt, m->kpl, m->ctx, m->gu, m->gated, m->pos};
   for (void* p : ps) if (p) (void)hipFree(p);
-  m->x = nullptr; m->h = nullptr; m->qkv = nullptr; m->vt = nullptr; m->ctx = nullptr; m->gu = nullptr;
+  m->x = nullptr; m->h = nullptr; m->qkv = nullptr; m->vt = nullptr; m->kpl = nullptr; m->ctx = nullptr; m->gu = nullptr;
   m->gated = nullptr; m->pos = nullptr;
   m->ws_rows = 0;
 }
@@ -531,6 +532,7 @@ int ensure_ws(eii_model* m, size_t rows) {
   al(&m->h, r * kD * 4);
   al((void**)&m->qkv, r * kQKVN * 2);
   al((void**)&m->vt, vt_bytes((int)r));
+  al((void**)&m->kpl, attn_kpl_bytes((int)r));
   al(&m->ctx, r * kD * 4);
   al((void**)&m->gu, r * 2 * kDFF * 2);
   al(&m->gated, r * kDFF * 4);
@@ -647,6 +649,7 @@ int run_block(eii_model* m, int l, int32_t* x, int M, int nseq, int max_T, const
     ProfScope ps(m, EII_K_ATTN, s);
     AttnArgs a{m->qkv, m->vt, m->seq_off, m->exp_tab, tr ? tr->attn_ctx : nullptr, (uint8_t*)m->ctx, M, nseq, max_T,
                m->max_kt, L.f[QR] + L.f[KR] + 3 - kFScore, 16 + L.f[VP] - L.f[CTX], L.bits[CTX]};
+    a.kpl = m->kpl;
     if (kv) {   // queries of the new positions against every cached key
       const int len = kv->p0 + kv->T_new;
       a.qkv = kv->kv->qkv[l];
@@ -657,6 +660,7 @@ int run_block(eii_model* m, int l, int32_t* x, int M, int nseq, int max_T, const
       a.max_kt = (len + 31) / 32;
       a.q_first = kv->p0;
       a.out_M = M;
+      a.kpl = nullptr;
     }
     HIPCHK(attention(a, s));
   }
@@ -1304,9 +1308,10 @@ extern "C" int eii_attention(const int16_t* qkv, const int32_t* seq_off, int nse
   }
   const int M = off[nseq];
   Staging st;
-  if ((rc = st.take(vt_bytes(M), s))) return rc;
+  if ((rc = st.take(Staging::align(vt_bytes(M)) + attn_kpl_bytes(M), s))) return rc;
   uint8_t* vt = st.carve<uint8_t>(vt_bytes(M));
   AttnArgs a{qkv, vt, seq_off, exp_tab, ctx, nullptr, M, nseq, max_T, max_kt, shift_s, 16 + f_v - f_c, bits_c};
+  a.kpl = st.carve<uint8_t>(attn_kpl_bytes(M));
   hipError_t e = build_vt(qkv, M, vt, s);
   if (e == hipSuccess) e = attention(a, s);
   if (e != hipSuccess) return fail(EII_E_DEVICE, std::string("eii_attention: ") + hipGetErrorString(e));

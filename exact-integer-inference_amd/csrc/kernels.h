@@ -150,7 +150,13 @@ struct AttnArgs {
   // the context of position t goes to row b (kv_len - q_first) + t - q_first of the ctx outputs,
   // which have out_M rows.
   int kv_len = 0, q_first = 0, out_M = 0;
+  // Plain forwards whose rows span more than 8 key tiles: a workspace of attn_kpl_bytes(M) bytes
+  // that the launcher fills with the k columns as limb planes (per row and kv group, 64 low bytes
+  // - 128 then 64 signed high bytes), read by the passes that recompute the scores; null = the
+  // kernel splits the k rows itself
+  uint8_t* kpl = nullptr;
 };
+inline size_t attn_kpl_bytes(int M) { return (size_t)M * 3 * 128; }
 // 32-row key tiles (aligned to multiples of 32 rows) spanned by a sequence at rows [s0, s0 + T)
 inline int attn_key_tiles(int s0, int T) { return ((s0 + T - 1) >> 5) - (s0 >> 5) + 1; }
 hipError_t attention(const AttnArgs& a, hipStream_t s);

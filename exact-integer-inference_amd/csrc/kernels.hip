@@ -1058,10 +1058,11 @@ __device__ __forceinline__ int32_t sum16x8(u32x4 d, int32_t s = 0) {   // s + th
   return s;
 }
 
-template <int OB, int NKT, int WPG, int KS = 1>
+template <int OB, int NKT, int WPG, int KS = 1, bool KP = false>
 __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) void attn_kernel(AttnArgs a) {
   static_assert(WPG == 1 || WPG == 4, "one wave per workgroup, or 4 waves");
   static_assert(KS == 1 || KS == WPG, "key tiles split over the waves of one task");
+  static_assert(!KP || NKT == 0, "k limb planes serve the recomputing passes");
   __shared__ int32_t etab[kDMax + 2];                              // exp table, etab[1537] = 0
   __shared__ __attribute__((aligned(16))) int32_t sklw[WPG][32];   // per wave: 128 * sum_d k per key
   __shared__ __attribute__((aligned(16))) v4i qxw[NKT == 0 ? WPG : 1][2][64];   // per wave: qx digits
@@ -1158,15 +1159,26 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
   }
 
   // K rows of key tile g for this lane (row pi(c) of the tile, d = 32 s + 16 h + 0..15), loaded
-  // one tile ahead of their use
+  // one tile ahead of their use: int16 values, or with KP their limb bytes (d[s][0] low, d[s][1] high)
   struct KRows { u32x4 d[2][2]; };
   const int16_t* const kbase = a.qkv + kD + kvg * 64 + 16 * h;   // row offsets below 2^31 elements
+  const uint8_t* const kpbase = KP ? a.kpl + kvg * 128 + 16 * h : nullptr;   // likewise bytes
   auto load_k = [&](int g, KRows& kr) __attribute__((always_inline)) {
-    const int16_t* kp = kbase + (uint32_t)min(32 * g + pic, a.M - 1) * (uint32_t)kQKVN;
+    const uint32_t row = (uint32_t)min(32 * g + pic, a.M - 1);
+    if constexpr (KP) {
+      const uint8_t* kp = kpbase + row * (uint32_t)(3 * 128);
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      kr.d[s][0] = *(const u32x4*)(kp + 32 * s);
-      kr.d[s][1] = *(const u32x4*)(kp + 32 * s + 8);
+      for (int s = 0; s < 2; ++s) {
+        kr.d[s][0] = *(const u32x4*)(kp + 32 * s);
+        kr.d[s][1] = *(const u32x4*)(kp + 64 + 32 * s);
+      }
+    } else {
+      const int16_t* kp = kbase + row * (uint32_t)kQKVN;
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        kr.d[s][0] = *(const u32x4*)(kp + 32 * s);
+        kr.d[s][1] = *(const u32x4*)(kp + 32 * s + 8);
+      }
     }
   };
   // Scores SAT16(RS(q.k, sh)) of key tile g for this lane's query, keys 16 h + j.  The sum
@@ -1181,6 +1193,11 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       const u32x4 d0 = kr.d[s][0], d1 = kr.d[s][1];
+      if constexpr (KP) {
+        kl[s] = __builtin_bit_cast(v4i, d0);
+        kh[s] = __builtin_bit_cast(v4i, d1);
+        continue;
+      }
       kl[s] = v4i{(int)lo_bytes16(d0[0], d0[1]), (int)lo_bytes16(d0[2], d0[3]), (int)lo_bytes16(d1[0], d1[1]),
                   (int)lo_bytes16(d1[2], d1[3])};
       kh[s] = v4i{(int)hi_bytes16(d0[0], d0[1]), (int)hi_bytes16(d0[2], d0[3]), (int)hi_bytes16(d1[0], d1[1]),
@@ -2002,6 +2019,22 @@ hipError_t attn_trace(const int16_t* qkv, int B, int T, const int32_t* exp_tab, 
   return hipGetLastError();
 }
 
+// k limb planes for the recomputing attention passes: thread = (row, kv group, 16 of its 64 k
+// columns); out row r at kpl + 384 r, kv group g at + 128 g: 64 bytes low - 128, then 64 high
+__global__ __launch_bounds__(256) void k_planes_kernel(const int16_t* qkv, int M, uint8_t* kpl) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (size_t)M * 12) return;
+  const size_t r = i / 12;
+  const int gc = (int)(i % 12), g = gc >> 2, c = gc & 3;
+  const int16_t* src = qkv + r * kQKVN + kD + 64 * g + 16 * c;
+  const u32x4 d0 = *(const u32x4*)src, d1 = *(const u32x4*)(src + 8);
+  uint8_t* dst = kpl + r * 384 + 128 * g + 16 * c;
+  *(u32x4*)dst = u32x4{lo_bytes16(d0[0], d0[1]), lo_bytes16(d0[2], d0[3]), lo_bytes16(d1[0], d1[1]),
+                       lo_bytes16(d1[2], d1[3])};
+  *(u32x4*)(dst + 64) = u32x4{hi_bytes16(d0[0], d0[1]), hi_bytes16(d0[2], d0[3]), hi_bytes16(d1[0], d1[1]),
+                              hi_bytes16(d1[2], d1[3])};
+}
+
 hipError_t attention(const AttnArgs& a, hipStream_t s) {
   if (a.B <= 0 || a.max_T <= 0) return hipSuccess;
   if (!a.vt || a.shift_s < 1 || a.shift_s > 30 || a.max_kt < 1) return hipErrorInvalidValue;
@@ -2048,12 +2081,28 @@ hipError_t attention(const AttnArgs& a, hipStream_t s) {
       if (a.bits_c == 16) hipLaunchKernelGGL((attn_kernel<2, 8, 4>), grid, block, 0, s, a);
       else hipLaunchKernelGGL((attn_kernel<4, 8, 4>), grid, block, 0, s, a);
     }
-  } else if (split) {
-    if (a.bits_c == 16) hipLaunchKernelGGL((attn_kernel<2, 0, 4, 4>), grid1, block, 0, s, a);
-    else hipLaunchKernelGGL((attn_kernel<4, 0, 4, 4>), grid1, block, 0, s, a);
   } else {
-    if (a.bits_c == 16) hipLaunchKernelGGL((attn_kernel<2, 0, 1>), grid1, block1, 0, s, a);
-    else hipLaunchKernelGGL((attn_kernel<4, 0, 1>), grid1, block1, 0, s, a);
+    // the recomputing passes read the k limb planes when the caller gives a workspace for them
+    const bool kp = a.kpl && !a.kv_len && attn_kpl_bytes(a.M) < ((size_t)1 << 31);
+    if (kp) {
+      const size_t n = (size_t)a.M * 12;
+      hipLaunchKernelGGL(k_planes_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a.qkv, a.M, a.kpl);
+    }
+    if (split) {
+      if (kp) {
+        if (a.bits_c == 16) hipLaunchKernelGGL((attn_kernel<2, 0, 4, 4, true>), grid1, block, 0, s, a);
+        else hipLaunchKernelGGL((attn_kernel<4, 0, 4, 4, true>), grid1, block, 0, s, a);
+      } else {
+        if (a.bits_c == 16) hipLaunchKernelGGL((attn_kernel<2, 0, 4, 4>), grid1, block, 0, s, a);
+        else hipLaunchKernelGGL((attn_kernel<4, 0, 4, 4>), grid1, block, 0, s, a);
+      }
+    } else if (kp) {
+      if (a.bits_c == 16) hipLaunchKernelGGL((attn_kernel<2, 0, 1, 1, true>), grid1, block1, 0, s, a);
+      else hipLaunchKernelGGL((attn_kernel<4, 0, 1, 1, true>), grid1, block1, 0, s, a);
+    } else {
+      if (a.bits_c == 16) hipLaunchKernelGGL((attn_kernel<2, 0, 1>), grid1, block1, 0, s, a);
+      else hipLaunchKernelGGL((attn_kernel<4, 0, 1>), grid1, block1, 0, s, a);
+    }
   }
   return hipGetLastError();
 }

@@ -593,20 +593,30 @@ struct KvStep {
   bool vt;
 };
 
+// At most 4 rows (decoding steps of up to 4 sequences) and no trace of the norm: the projection
+// after an RMSNorm forms the normalized rows from x itself (GemmArgs::nx), in the rmsnorm
+// launcher's fast path (gains in int16, which the loader enforces; output shift 10..40) for
+// 16-bit norm outputs
+bool fuse_norm(int M, int sh_out, int bits, const eii_trace* tr) {
+  return !tr && M <= 4 && bits == 16 && sh_out >= 10 && sh_out <= 40;
+}
+
 int run_block(eii_model* m, int l, int32_t* x, int M, int nseq, int max_T, const eii_trace* tr, hipStream_t s,
               const KvStep* kv = nullptr) {
   const Layer& L = m->L[l];
   const int hb = L.bits[NORM1] / 8;
   uint8_t* h = (uint8_t*)m->h;
-  {
+  const int sh_n1 = 21 + L.ln1_f - L.f[NORM1], sh_n2 = 21 + L.ln2_f - L.f[NORM2];
+  if (!fuse_norm(M, sh_n1, L.bits[NORM1], tr)) {
     ProfScope ps(m, EII_K_NORM, s);
-    HIPCHK(rmsnorm(x, M, L.ln1, 21 + L.ln1_f - L.f[NORM1], L.bits[NORM1], h, tr ? tr->norm1_out : nullptr, s, false,
+    HIPCHK(rmsnorm(x, M, L.ln1, sh_n1, L.bits[NORM1], h, tr ? tr->norm1_out : nullptr, s, false,
                    tr ? tr->norm1_U : nullptr, tr ? tr->norm1_z : nullptr));
   }
   const int sh_q = 30 + L.f[QP] - L.f[QR], sh_k = 30 + L.f[KP] - L.f[KR];
   {
     ProfScope ps(m, EII_K_GEMM_QKV, s);
     GemmArgs g = gemm_args(L.qkv, h, M, m->qkv, 16);
+    if (fuse_norm(M, sh_n1, L.bits[NORM1], tr)) { g.nx = x; g.ngain = L.ln1; g.nsh = sh_n1; }
     if (!tr) {   // q, k, v projections with RoPE and the V^T planes in the epilogue
       g.pos = m->pos; g.cosT = m->rope_c; g.sinT = m->rope_s; g.sh_q = sh_q; g.sh_k = sh_k;
       if (!kv) { g.vt = m->vt; g.vt_stride = vt_stride_for(M); }
@@ -678,9 +688,9 @@ int run_block(eii_model* m, int l, int32_t* x, int M, int nseq, int max_T, const
   }
   if (tr && tr->resid_mid) HIPCHK(hipMemcpyAsync(tr->resid_mid, x, (size_t)M * kD * 4, hipMemcpyDeviceToDevice, s));
   const int h2b = L.bits[NORM2] / 8;
-  {
+  if (!fuse_norm(M, sh_n2, L.bits[NORM2], tr)) {
     ProfScope ps(m, EII_K_NORM, s);
-    HIPCHK(rmsnorm(x, M, L.ln2, 21 + L.ln2_f - L.f[NORM2], L.bits[NORM2], h, tr ? tr->norm2_out : nullptr, s, false,
+    HIPCHK(rmsnorm(x, M, L.ln2, sh_n2, L.bits[NORM2], h, tr ? tr->norm2_out : nullptr, s, false,
                    tr ? tr->norm2_U : nullptr, tr ? tr->norm2_z : nullptr));
   }
   const int gb = L.bits[GATED] / 8;
@@ -690,6 +700,7 @@ int run_block(eii_model* m, int l, int32_t* x, int M, int nseq, int max_T, const
     if (!tr) {   // gate and up projections with the SiLU table and the gated product in the epilogue
       GemmArgs g = gemm_args(L.gu, h, M, m->gated, 16);
       g.aux_tab = L.silu; g.sh2 = sh_s; g.bits2 = L.bits[GATED]; g.tab_bits = L.bits[SILU];
+      if (fuse_norm(M, sh_n2, L.bits[NORM2], tr)) { g.nx = x; g.ngain = L.ln2; g.nsh = sh_n2; }
       HIPCHK(gemm(g, h2b, EPI_SILU, s));
     } else {
       HIPCHK(gemm(gemm_args(L.gu, h, M, m->gu, 16), h2b, EPI_REQ16, s));
@@ -715,12 +726,15 @@ int run_block(eii_model* m, int l, int32_t* x, int M, int nseq, int max_T, const
 }
 
 int run_final(eii_model* m, const int32_t* x, int M, int32_t* logits, hipStream_t s) {
-  {
+  const int sh_n = 21 + m->fg_f - m->f_y;
+  const bool fused = fuse_norm(M, sh_n, 16, nullptr);
+  if (!fused) {
     ProfScope ps(m, EII_K_NORM, s);
-    HIPCHK(rmsnorm(x, M, m->fg, 21 + m->fg_f - m->f_y, 16, (uint8_t*)m->h, nullptr, s));
+    HIPCHK(rmsnorm(x, M, m->fg, sh_n, 16, (uint8_t*)m->h, nullptr, s));
   }
   GemmArgs g = gemm_args(m->head, m->h, M, logits, 32);
   g.flag = m->flags;
+  if (fused) { g.nx = x; g.ngain = m->fg; g.nsh = sh_n; }
   ProfScope ps(m, EII_K_GEMM_HEAD, s);
   HIPCHK(gemm(g, 2, EPI_LOGITS, s));
   return EII_OK;

@@ -74,6 +74,12 @@ struct GemmArgs {
   int a_kb = 64;
   // row blocks per group of the tile order (set by the launch)
   int tile_g = 8;
+  // RMSNorm folded into the GEMM (K = 576, a_bytes 2, at most 4 rows: a wave per row in the
+  // prologue): A is SAT(RS(3 RS(x U, 16) gain, nsh), 16) of x [M, 576] (the rmsnorm launcher's
+  // values for gains in int16 and nsh in 10..40), formed from x instead of read as limb planes
+  const int32_t* nx = nullptr;
+  const int32_t* ngain = nullptr;
+  int nsh = 0;
 };
 
 // V^T limb planes for attention: plane 0 = low bytes - 128, plane 1 = signed high bytes of v;

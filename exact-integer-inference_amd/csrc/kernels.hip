@@ -50,6 +50,27 @@ __device__ __forceinline__ uint32_t limb_word(const int32_t* v, int l, int W) {
          (limb_byte(v[3], l, W) << 24);
 }
 
+// v + the value of the lane that DPP control CTRL selects, for an int64 moved as two dwords
+template <int CTRL>
+__device__ __forceinline__ int64_t dpp_add64(int64_t v) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)v, CTRL, 0xF, 0xF, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)((uint64_t)v >> 32), CTRL, 0xF, 0xF, false);
+  return v + (int64_t)(((uint64_t)hi << 32) | lo);
+}
+// sum over each group of LPR lanes (16 or 64), in every lane of the group: within 16-lane rows by
+// DPP (lane ^ 1, lane ^ 2, then the mirrored lane of the other quad of the 8 and of the other 8 of
+// the row), across rows by lane shuffles
+template <int LPR>
+__device__ __forceinline__ int64_t group_sum64(int64_t v) {
+  v = dpp_add64<0xB1>(v);    // quad_perm [1, 0, 3, 2]
+  v = dpp_add64<0x4E>(v);    // quad_perm [2, 3, 0, 1]
+  v = dpp_add64<0x141>(v);   // row_half_mirror
+  v = dpp_add64<0x140>(v);   // row_mirror
+  if constexpr (LPR > 16) v += __shfl_xor(v, 16);
+  if constexpr (LPR > 32) v += __shfl_xor(v, 32);
+  return v;
+}
+
 // ------------------------------------------------------------------------------ GEMM
 // Persistent workgroups of 4 waves, two per CU, sweep BM x BN output tiles (128 x 128 for 2-limb
 // activations, 64 x 128 for 4-limb, 64 x 192 for 2-limb residual GEMMs with N = 576) in a flat
@@ -109,9 +130,10 @@ __device__ __forceinline__ void tile_coords(int v, int nMB, int nNB, int G, int&
 
 __device__ __forceinline__ uint32_t pack16(int32_t a, int32_t b) { return (uint32_t)(a & 0xFFFF) | ((uint32_t)b << 16); }
 
-template <int AW, int EPI, int NK, int SHAPE>
+template <int AW, int EPI, int NK, int SHAPE, bool NORM = false>
 __global__ __launch_bounds__(256, SHAPE == kShapeSkinny || SHAPE == kShapeSkinny32 ? 1 : 2) void gemm_kernel(GemmArgs g) {
   using C = GemmCfg<AW, SHAPE>;
+  static_assert(!NORM || (C::kSkinny && NK == 9 && AW == 2), "the RMSNorm prologue: skinny tiles, K = 576, 16-bit");
   static_assert(SHAPE != kShapeNarrow || EPI == EPI_RESID || EPI == EPI_I64 || EPI == EPI_REQ16 ||
                 EPI == EPI_REQ32 || EPI == EPI_LOGITS,
                 "the SiLU and QKV epilogues pair columns 32 apart within 64-column blocks");
@@ -123,7 +145,10 @@ __global__ __launch_bounds__(256, SHAPE == kShapeSkinny || SHAPE == kShapeSkinny
   // LDS beside two workgroups' stages, and about 0.3 % of the gates lie outside it)
   constexpr int kTabHalf = 4096;
   constexpr int kTabBytes = kSilu ? 4 * kTabHalf : 0;
-  __shared__ __attribute__((aligned(16))) uint8_t smem[C::kStages * C::kStage + kTabBytes];
+  // skinny tiles: the RMSNorm prologue's limb bytes of up to kNormRows rows after the reduction area
+  constexpr int kNormRows = 4;
+  constexpr int kNormBytes = NORM ? AW * kNormRows * kD : 0;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[C::kStages * C::kStage + kTabBytes + kNormBytes];
   const int nMB = (g.M + C::BM - 1) / C::BM, nNB = (g.N + C::BN - 1) / C::BN, nT = nMB * nNB;
   // this workgroup's tiles: v = v0, v0 + stride, ... < vend (kShapeSkinny: tile blockIdx.x alone)
   const int xcd = blockIdx.x & 7, per = (nT + 7) / 8, nwg_x = C::kSkinny ? 1 : gridDim.x >> 3;
@@ -563,15 +588,60 @@ __global__ __launch_bounds__(256, SHAPE == kShapeSkinny || SHAPE == kShapeSkinny
     for (int i = 0; i < NSW; ++i)
       if (i < cnt) {
         const int sl = s0 + i;
-        const size_t aoff = a_src_off(0, m, sl >> 1, 2 * (sl & 1) + fh, g.M, g.a_kb, 0);
+        if constexpr (!NORM) {
+          const size_t aoff = a_src_off(0, m, sl >> 1, 2 * (sl & 1) + fh, g.M, g.a_kb, 0);
 #pragma unroll
-        for (int l = 0; l < AW; ++l) af[i][l] = *(const v4i*)(Ab + (size_t)l * g.a_plane + aoff);
+          for (int l = 0; l < AW; ++l) af[i][l] = *(const v4i*)(Ab + (size_t)l * g.a_plane + aoff);
+        }
 #pragma unroll
         for (int tn = 0; tn < C::TN; ++tn) {
           const int nb32 = min(nb * C::TN + tn, nb32_last);
           wf[i][tn] = *(const v4i*)(g.W + w_frag(nb32, kslices, sl, lane));
         }
       }
+    if constexpr (NORM) {
+      // the values of rmsnorm_kernel's fast path with a wave per row (rmsnorm_kernel<., false,
+      // 64>): wave w normalizes tile row w (lane c: columns 64 k + c) and leaves its limb bytes in
+      // LDS, where the lanes of every wave read their fragments (rows past M: zero)
+      const int R = min(g.M - mb * C::BM, kNormRows);
+      uint8_t* stg = smem + C::kStages * C::kStage + kTabBytes;   // [2][kNormRows][576] limb bytes
+      if (wave < R) {
+        const int32_t* xr = g.nx + (size_t)(mb * C::BM + wave) * kD + lane;
+        int32_t v[9], gv[9];
+#pragma unroll
+        for (int k = 0; k < 9; ++k) {
+          v[k] = xr[64 * k];
+          gv[k] = 3 * g.ngain[64 * k + lane];
+        }
+        int64_t SA = 0, SB = 0, SC = 0;
+#pragma unroll
+        for (int k = 0; k < 9; ++k) {
+          const int32_t hi = v[k] >> 16, lo = v[k] & 0xFFFF;
+          SA += (int64_t)hi * hi; SB += (int64_t)hi * lo; SC += (int64_t)lo * lo;
+        }
+        SA = group_sum64<64>(SA);
+        SB = group_sum64<64>(SB);
+        SC = group_sum64<64>(SC);
+        const int32_t U = (int32_t)norm_U(norm_total(SA, SB, SC));   // < 2^29
+        const int64_t rnd = (int64_t)1 << (g.nsh - 1);
+#pragma unroll
+        for (int k = 0; k < 9; ++k) {
+          const int32_t z = (int32_t)(((int64_t)v[k] * U + 32768) >> 16);
+          const int32_t q = (int32_t)(((int64_t)z * gv[k] + rnd) >> g.nsh);
+          const int32_t o = min(max(q, -32768), 32767);
+#pragma unroll
+          for (int l = 0; l < AW; ++l) stg[(l * kNormRows + wave) * kD + 64 * k + lane] = (uint8_t)limb_byte(o, l, AW);
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < NSW; ++i)
+        if (i < cnt) {
+#pragma unroll
+          for (int l = 0; l < AW; ++l)
+            af[i][l] = fc < R ? *(const v4i*)(stg + (l * kNormRows + fc) * kD + 32 * (s0 + i) + 16 * fh) : v4i{};
+        }
+    }
     // wave 0 reads the epilogue's per-column coefficients and, lane c for tile row c, the residual
     // row or the position and its RoPE rows while the operands load, so the epilogue's own reads of
     // them hit the CU's cache instead of adding memory round trips after the reduction
@@ -743,7 +813,12 @@ hipError_t launch_gemm_cfg(const GemmArgs& a_in, hipStream_t s) {
   // (576, 1536) for every epilogue, and 64, 128 for the operator entry points
   constexpr bool op = EPI == EPI_I64 || EPI == EPI_REQ16 || EPI == EPI_REQ32;
   switch (a.K / kBK) {
-    case 9: hipLaunchKernelGGL((gemm_kernel<AW, EPI, 9, SHAPE>), grid, block, 0, s, a); break;
+    case 9:
+      if constexpr (AW == 2 && C::kSkinny && (EPI == EPI_QKV || EPI == EPI_SILU || EPI == EPI_SILU_I || EPI == EPI_LOGITS))
+        if (a.nx) { hipLaunchKernelGGL((gemm_kernel<AW, EPI, 9, SHAPE, true>), grid, block, 0, s, a); break; }
+      if (a.nx) return hipErrorInvalidValue;
+      hipLaunchKernelGGL((gemm_kernel<AW, EPI, 9, SHAPE>), grid, block, 0, s, a);
+      break;
     case 24: hipLaunchKernelGGL((gemm_kernel<AW, EPI, 24, SHAPE>), grid, block, 0, s, a); break;
     case 1: if constexpr (op) { hipLaunchKernelGGL((gemm_kernel<AW, EPI, 1, SHAPE>), grid, block, 0, s, a); break; }
             return hipErrorInvalidValue;
@@ -763,9 +838,11 @@ hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
   // decoding step: 3.08 -> 2.08 ms), except for the head beyond 32 rows, whose 28 MB of weights each
   // 32-row block would read again (the 64-row tiles read them half as often)
   if (a.M <= 256 && (EPI != EPI_LOGITS || a.M <= 32)) {
+    if (a.nx && (a.K != 576 || a.M > 4 || !a.ngain || a.nsh < 10 || a.nsh > 40)) return hipErrorInvalidValue;
     if constexpr (EPI == EPI_SILU || EPI == EPI_SILU_I || EPI == EPI_QKV) return launch_gemm_cfg<AW, EPI, kShapeSkinny>(a, s);
     else return launch_gemm_cfg<AW, EPI, kShapeSkinny32>(a, s);
   }
+  if (a.nx) return hipErrorInvalidValue;   // the RMSNorm prologue is a skinny-tile one
   if constexpr (AW == 2 && EPI == EPI_RESID)
     if (a.N % 192 == 0 && a.N % 128 != 0) return launch_gemm_cfg<AW, EPI, kShapeNarrow>(a, s);
   if constexpr (AW == 2 && EPI != EPI_RESID)
@@ -865,26 +942,6 @@ __global__ __launch_bounds__(256) void embed_kernel(const int64_t* ids, int M, c
 }
 
 // ------------------------------------------------------------------------------ rmsnorm
-// v + the value of the lane that DPP control CTRL selects, for an int64 moved as two dwords
-template <int CTRL>
-__device__ __forceinline__ int64_t dpp_add64(int64_t v) {
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)v, CTRL, 0xF, 0xF, false);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)((uint64_t)v >> 32), CTRL, 0xF, 0xF, false);
-  return v + (int64_t)(((uint64_t)hi << 32) | lo);
-}
-// sum over each group of LPR lanes (16 or 64), in every lane of the group: within 16-lane rows by
-// DPP (lane ^ 1, lane ^ 2, then the mirrored lane of the other quad of the 8 and of the other 8 of
-// the row), across rows by lane shuffles
-template <int LPR>
-__device__ __forceinline__ int64_t group_sum64(int64_t v) {
-  v = dpp_add64<0xB1>(v);    // quad_perm [1, 0, 3, 2]
-  v = dpp_add64<0x4E>(v);    // quad_perm [2, 3, 0, 1]
-  v = dpp_add64<0x141>(v);   // row_half_mirror
-  v = dpp_add64<0x140>(v);   // row_mirror
-  if constexpr (LPR > 16) v += __shfl_xor(v, 16);
-  if constexpr (LPR > 32) v += __shfl_xor(v, 32);
-  return v;
-}
 // LPR lanes per row: 16 (4 rows per wave, for many rows) or 64 (a wave per row: a quarter of the
 // serial work per lane, for the few rows of a decoding step).  Lane c of a row holds the VW = 64 /
 // LPR columns 64 k + VW c .. + VW - 1, k = 0..8, so loads are 4 VW bytes, the limb bytes of a

@@ -144,7 +144,9 @@ __global__ __launch_bounds__(256, SHAPE == kShapeSkinny || SHAPE == kShapeSkinny
   // after the stages (the gate values cluster around 0: with 64 x 256 tiles the window fills the CU's
   // LDS beside two workgroups' stages, and about 0.3 % of the gates lie outside it)
   constexpr int kTabHalf = 4096;
-  constexpr int kTabBytes = kSilu ? 4 * kTabHalf : 0;
+  // EPI_SILU keeps the window as int32 (16- and 32-bit tables), EPI_SILU_I as int16
+  using TabT = std::conditional_t<EPI == EPI_SILU, int32_t, int16_t>;
+  constexpr int kTabBytes = kSilu ? 2 * kTabHalf * (int)sizeof(TabT) : 0;
   // skinny tiles: the RMSNorm prologue's limb bytes of up to kNormRows rows after the reduction area
   constexpr int kNormRows = 4;
   constexpr int kNormBytes = NORM ? AW * kNormRows * kD : 0;
@@ -157,12 +159,12 @@ __global__ __launch_bounds__(256, SHAPE == kShapeSkinny || SHAPE == kShapeSkinny
   if (v0 >= vend) return;
   const int ntiles = (vend - v0 + nwg_x - 1) / nwg_x;
   constexpr int nk = NK;
-  int16_t* const tabw = (int16_t*)(smem + C::kStages * C::kStage);
-  int tab_half = 0;   // 0: no LDS window (32-bit table), every read goes to global memory
+  TabT* const tabw = (TabT*)(smem + C::kStages * C::kStage);
+  int tab_half = 0;   // 0: no LDS window, every read goes to global memory
   if constexpr (kSilu) {
-    if (!C::kSkinny && g.tab_bits == 16) {   // (a skinny tile's few rows read the table in global memory)
+    if (!C::kSkinny) {   // (a skinny tile's few rows read the table in global memory)
       tab_half = kTabHalf;
-      for (int i = threadIdx.x; i < 2 * kTabHalf; i += C::kThreads) tabw[i] = (int16_t)g.aux_tab[32768 - kTabHalf + i];
+      for (int i = threadIdx.x; i < 2 * kTabHalf; i += C::kThreads) tabw[i] = (TabT)g.aux_tab[32768 - kTabHalf + i];
     }
     __syncthreads();
   }

@@ -1242,11 +1242,17 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
   };
   // Scores SAT16(RS(q.k, sh)) of key tile g for this lane's query, keys 16 h + j.  The sum
   // acc + 2^(sh-1) = 65536 wv + lo16 with lo16 in [0, 65536) is evaluated in int32 pieces.
-  // RAW (shift >= 16 only): sc = the high parts wv, whose shifted and clamped values are the
-  // scores; the row max of the scores is that of wv, shifted and clamped (both maps are monotone)
-  auto scores = [&](int g, const KRows& kr, int32_t (&sc)[16], auto RAW) __attribute__((always_inline)) {
-    constexpr bool raw = decltype(RAW)::value;
-    constexpr int32_t masked = raw ? INT32_MIN : kMasked;
+  // MODE Raw (shift >= 16 only): sc = the high parts wv, whose shifted and clamped values are the
+  // scores; the row max of the scores is that of wv, shifted and clamped (both maps are monotone).
+  // MODE Dist: sc = the exp table index d = min(rm - score, 1537) for the row max rm, masked keys
+  // 1537 (entry 0).  For shift >= 16 with s' = wv >> (sh - 16) and score = SAT16(s'), d is
+  // med3(rm - s', rm - 32767, min(1537, rm + 32768)): s' in range gives min(rm - s', 1537)
+  // (rm - s' <= rm + 32768); s' > 32767 means rm = 32767 and d = 0 = rm - 32767; s' < -32768 gives
+  // min(1537, rm + 32768).  One median instead of a clamp, a difference and a min.
+  auto scores = [&](int g, const KRows& kr, int32_t (&sc)[16], auto MODE, int32_t rm = 0) __attribute__((always_inline)) {
+    constexpr int mode = decltype(MODE)::value;
+    constexpr bool raw = mode == 1;
+    constexpr int32_t masked = raw ? INT32_MIN : mode == 2 ? kDMax + 1 : kMasked;
     v4i kl[2], kh[2];
     int32_t ks = 0;
 #pragma unroll
@@ -1305,6 +1311,10 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
     if constexpr (raw) {
 #pragma unroll
       for (int j = 0; j < 16; ++j) sc[j] = wv[j];
+    } else if (mode == 2 && sh >= 16) {
+      const int32_t dl = rm - 32767, dh = min(kDMax + 1, rm + 32768);
+#pragma unroll
+      for (int j = 0; j < 16; ++j) sc[j] = min(max(rm - (wv[j] >> (sh - 16)), dl), dh);
     } else if (sh >= 16) {
 #pragma unroll
       for (int j = 0; j < 16; ++j) sc[j] = min(max(wv[j] >> (sh - 16), -32768), 32767);
@@ -1312,6 +1322,10 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
 #pragma unroll
       for (int j = 0; j < 16; ++j)
         sc[j] = min(max(min(max(wv[j], -32769), 32768) * (1 << (16 - sh)) + ((lo[j] & 0xFFFF) >> sh), -32768), 32767);
+      if constexpr (mode == 2) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) sc[j] = min(rm - sc[j], kDMax + 1);
+      }
     }
     // keys past the query (the diagonal tile) and before the sequence start (its first tile when
     // the sequence does not start on a tile boundary): key 32 g + 16 h + j
@@ -1328,17 +1342,9 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
         if (j < first) sc[j] = masked;
     }
   };
-  using Raw = std::true_type;
-  using Full = std::false_type;
-  // e = E[rowmax - s] for d <= 1536, else 0; masked keys 0
-  auto expo = [&](int g, int j, int32_t s, int32_t rowmax) __attribute__((always_inline)) -> int32_t {
-    const int32_t e = etab[min(rowmax - s, kDMax + 1)];
-    if (32 * g < s0 || 32 * g + 31 > q0) {
-      const int key = 32 * g + 16 * h + j;
-      if (key < s0 || key > qi) return 0;
-    }
-    return e;
-  };
+  using Full = std::integral_constant<int, 0>;
+  using Raw = std::integral_constant<int, 1>;
+  using Dist = std::integral_constant<int, 2>;
 
   v16i C16[2], C8[2], C0[2];
 #pragma unroll
@@ -1518,8 +1524,8 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
     return true;
   };
 
-  // Long rows: every pass recomputes the scores; the exp lookups test keys only in waves with a
-  // row max near -32768 (see the register-resident passes below).  The row-max and exp-sum passes
+  // Long rows: every pass recomputes the scores, which the exp-sum and P.V passes take as exp table
+  // indices (MODE Dist: masked keys at the zero entry, so no key tests).  The row-max and exp-sum passes
   // load the K rows of the wave's next tile while the current one computes (two slots per
   // iteration, so the buffer of each is a compile-time choice); the P.V pass, whose registers hold
   // the context sums, loads each tile's K and V at its start.
@@ -1547,11 +1553,9 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
     if (sh >= 16) rowmax = min(max(max_pass(Raw{}) >> (sh - 16), -32768), 32767);
     else rowmax = max_pass(Full{});
     rowmax = combine_max(max(rowmax, __shfl_xor(rowmax, 32)));
-    auto passes = [&](auto CLEAN) __attribute__((always_inline)) {
-      auto ex = [&](int t, int j, int32_t s) __attribute__((always_inline)) -> uint32_t {
-        if constexpr (decltype(CLEAN)::value) return (uint32_t)etab[min(rowmax - s, kDMax + 1)];
-        else return (uint32_t)expo(g0 + tg(t), j, s, rowmax);
-      };
+    {
+      // the scores come as exp table indices (masked keys: the zero entry)
+      auto ex = [&](int d) __attribute__((always_inline)) -> uint32_t { return (uint32_t)etab[d]; };
       uint64_t Z = 0;   // e <= 2^30: sums of three fit uint32
       if (KS == 1 || nloc > 0) load_k(g0 + tg(0), kb[0]);
 #pragma unroll 1
@@ -1562,10 +1566,10 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
           if (t < nloc) {
             if (t + 1 < nloc) load_k(g0 + tg(t + 1), kb[u ^ 1]);
             int32_t sc[16];
-            scores(g0 + tg(t), kb[u], sc, Full{});
+            scores(g0 + tg(t), kb[u], sc, Dist{}, rowmax);
 #pragma unroll
-            for (int j = 0; j < 15; j += 3) Z += ex(t, j, sc[j]) + ex(t, j + 1, sc[j + 1]) + ex(t, j + 2, sc[j + 2]);
-            Z += ex(t, 15, sc[15]);
+            for (int j = 0; j < 15; j += 3) Z += ex(sc[j]) + ex(sc[j + 1]) + ex(sc[j + 2]);
+            Z += ex(sc[15]);
           }
         }
       }
@@ -1575,14 +1579,12 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
         int32_t sc[16];
         load_k(g0 + tg(t), kr[0]);
         load_v(g0 + tg(t), vf[0]);
-        scores(g0 + tg(t), kr[0], sc, Full{});
+        scores(g0 + tg(t), kr[0], sc, Dist{}, rowmax);
 #pragma unroll
-        for (int j = 0; j < 16; ++j) sc[j] = (int32_t)ex(t, j, sc[j]);
+        for (int j = 0; j < 16; ++j) sc[j] = (int32_t)ex(sc[j]);
         pv(vf[0], sc);
       }
-    };
-    if (__all(rowmax > kMasked + kDMax)) passes(std::true_type{});
-    else passes(std::false_type{});
+    }
   };
   if constexpr (NKT > 0) {
     constexpr int NT = (NKT + KS - 1) / KS;   // key tiles per wave

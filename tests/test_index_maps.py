@@ -82,6 +82,36 @@ def test_attention_score_digits(hc):
     assert hc.eii_host_attn_digits(11, 1) > 0         # planted: the extra 0/1 digit of q >= 32640 dropped
 
 
+def _dist_table_index(rm, sp, hi_bound=True):
+    # kernels.hip attn_kernel scores(), MODE Dist, score shift >= 16: s' = wv >> (sh - 16) and the
+    # exp table index as one median of three
+    hi = np.minimum(1537, rm + 32768) if hi_bound else np.full_like(rm, 1537)
+    return np.clip(rm - sp, rm - 32767, hi)
+
+
+def test_attention_table_index_median():
+    # the index the exp lookups use, min(rowmax - SAT16(s'), 1537) (python/intref.py:239-244, with
+    # index 1537 holding 0), for every shifted score s' of the int32 range the kernels form and
+    # every row max that is the max of its row's saturated scores (rm >= SAT16(s'))
+    rng = np.random.default_rng(16)
+    sp = np.concatenate([rng.integers(-2**31, 2**31, 400000), np.arange(-34000, 34000),
+                         [-2**31, 2**31 - 1, -32769, -32768, 32767, 32768]]).astype(np.int64)
+    rm = np.concatenate([rng.integers(-32768, 32768, sp.size - 8), [-32768, -32768, -31232, -31231, 32767, 32767,
+                                                                     0, -1]]).astype(np.int64)
+    sat = np.clip(sp, -32768, 32767)
+    rm = np.maximum(rm, sat)   # a row max is at least every score of its row
+    want = np.minimum(rm - sat, 1537)
+    assert np.array_equal(_dist_table_index(rm, sp), want)
+    # every row max from -32768 upward against the scores that saturate low and high
+    rm2 = np.arange(-32768, 32768, dtype=np.int64)
+    for s in (-2**31, -40000, -32769, -32768):
+        assert np.array_equal(_dist_table_index(rm2, np.full_like(rm2, s)), np.minimum(rm2 + 32768, 1537))
+    assert np.array_equal(_dist_table_index(np.array([32767]), np.array([2**31 - 1])), np.array([0]))
+    # planted: the upper bound without rm + 32768 (rows whose max lies within 1536 of -32768)
+    assert not np.array_equal(_dist_table_index(rm2, np.full_like(rm2, -40000), hi_bound=False),
+                              np.minimum(rm2 + 32768, 1537))
+
+
 @pytest.mark.parametrize("N,K", [(576, 576), (960, 576), (100, 64), (33, 1536)])
 def test_weight_fragment_order(hc, N, K):
     assert hc.eii_host_wfrag_model(N, K) == 0

@@ -362,7 +362,7 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py: this engine runs on one GPU (sequences shard across GPUs with no exchange, "
-              f"which this build does not launch); --gpus {args.gpus} is not supported", file=sys.stderr)
+              f"which this program does not launch); --gpus {args.gpus} is not supported", file=sys.stderr)
         sys.exit(2)
 
     import torch

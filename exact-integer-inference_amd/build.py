@@ -3,12 +3,12 @@ libeii_hostcheck.so in place.
 
     python build.py                              # everything, next to this file
     python build.py --out DIR --opt="-O1 ..."    # libeii.so + eii_check into DIR, the HIP
-                                                 # sources and the checker compiled with these
+                                                 # sources and eii_check compiled with these
                                                  # optimization flags instead of -O3 / -O2 (the
                                                  # build variants of python -m eii.conformance)
 
 hipcc applies a plain -O level to the host and the device code alike; "-Xarch_host -O0" after it
-lowers the host code only (the engine, the C ABI and the checker) and leaves the device code at
+lowers the host code only (the engine, the C ABI and eii_check) and leaves the device code at
 the level before it.
 """
 import argparse

@@ -15,7 +15,7 @@
  * RMSNorm sum of squares in 128 bits with an integer square root, the softmax division as an
  * integer division.  Rows (tokens) are independent everywhere except in attention, which runs
  * per head and query; OpenMP spreads both over the host's cores.  Only tests/ and bench.py's CPU
- * baseline run it, as the checker; the GPU engine never does.
+ * baseline run it, to check the GPU engine's states; the engine never does.
  */
 #include <stdint.h>
 #include <stdio.h>

@@ -1,7 +1,7 @@
 """ORACLE (test infrastructure only): numpy restatement of python/intref.py.
 
 Only tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg import this module,
-and only as the checker of the HIP engine; the engine never calls it.
+and only to check the HIP engine's results; the engine never calls it.
 
 It restates the integer semantics of python/intref.py step by step (each function cites
 the lines it follows) over a model.bin image read by its own reader (the layout of

@@ -79,7 +79,7 @@ def test_reference_c_accepts_oracle_states(cfg1_states, model_path):
         r = subprocess.run([REF_BIN, d, d], capture_output=True, text=True, timeout=300)
         assert r.returncode == 0, r.stdout[-2000:]
         assert "ALL STATES EXACT" in r.stdout
-        # the checker is not vacuous: one changed logit is reported
+        # the comparison is not vacuous: one changed logit is reported
         bad = lg[0].astype(np.int32).copy()
         bad[3, 17] += 1
         bad.tofile(os.path.join(d, "exp_logits.i32"))

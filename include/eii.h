@@ -137,7 +137,8 @@ int eii_argmax(const int32_t* logits_dev, int rows, int n, int64_t* out_dev, voi
 
 /* ---- operator level (python/intref.py functions) ----
  * eii_gemm_i8, eii_gemm_i8_ws, eii_linear and eii_attention stage their operands (limb planes,
- * weights in fragment order, V^T planes) in one device block per GPU that the library keeps for
+ * weights in fragment order, V^T planes and, for attention, k limb planes) in one device block
+ * per GPU that the library keeps for
  * the life of the process and grows with hipMalloc when a call needs more; calls at sizes seen
  * before allocate nothing.  Calls on one GPU take the block in turn: each call's stream waits for
  * the previous call's work, whichever stream that was on. */

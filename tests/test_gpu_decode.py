@@ -76,6 +76,22 @@ def test_chunked_appends_equal_full_forward(eng, chunks):
         kv.close()
 
 
+@pytest.mark.parametrize("B", [4, 5])
+def test_few_sequences_single_steps_equal_full_forward(eng, B):
+    # single-token steps of up to 4 sequences fold the RMSNorm into the q/k/v, gate/up and head
+    # GEMMs (a wave per row in their prologue); 5 sequences take the rmsnorm launches
+    ids = torch.from_numpy(np.random.default_rng(40 + B).integers(0, 49152, size=(B, 44), dtype=np.int64)).to(eng.device)
+    full = eng.forward(ids)["logits"]
+    kv = eng.kv_cache(B, 44)
+    try:
+        kv.append(ids[:, :36], logits=False)
+        for t in range(36, 44):
+            lg = kv.append(ids[:, t:t + 1])
+            assert torch.equal(lg[:, 0], full[:, t]), t
+    finally:
+        kv.close()
+
+
 def test_many_sequences_single_steps_equal_full_forward(eng):
     # 96 sequences: the decoding attention runs one wave per head (few sequences take four)
     ids = torch.from_numpy(np.random.default_rng(96).integers(0, 49152, size=(96, 70), dtype=np.int64)).to(eng.device)

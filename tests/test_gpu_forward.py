@@ -87,3 +87,21 @@ def test_forward_ragged_batch(engine, oracle):
         sl = slice(off[b], off[b + 1])
         assert first_diff(res[:, sl], r1[:, 0]) is None, f"sequence {b}"
         assert first_diff(lg[sl], l1[0]) is None, f"sequence {b}"
+
+
+@pytest.mark.parametrize("lens", [[3], [2, 1, 1]])
+def test_forward_few_rows(engine, oracle, lens):
+    # at most 4 rows: the q/k/v, gate/up and head GEMMs form the RMSNorm in their prologue (a
+    # plain forward, so the q/k/v epilogue also writes the V^T planes); every residual and logit
+    # against the oracle's runs of each sequence
+    rng = np.random.default_rng(3 + len(lens))
+    ids = [rng.integers(0, 49152, size=t, dtype=np.int64) for t in lens]
+    out = engine.forward_packed(np.concatenate(ids), lens, resid=True, logits=True)
+    res = out["resid"].cpu().numpy()
+    lg = out["logits"].cpu().numpy()
+    off = np.concatenate([[0], np.cumsum(lens)])
+    for b, t in enumerate(lens):
+        _, r1, l1 = oracle.forward(ids[b][None, :])
+        sl = slice(off[b], off[b + 1])
+        assert first_diff(res[:, sl], r1[:, 0]) is None, f"sequence {b}"
+        assert first_diff(lg[sl], l1[0]) is None, f"sequence {b}"

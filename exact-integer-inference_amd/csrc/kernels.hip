@@ -1155,9 +1155,17 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
   const int s0 = a.seq_off[seq], T = a.kv_len ? a.kv_len : a.seq_off[seq + 1] - s0;
   idle = idle || 32 * qt >= T;
   if ((WPG == 1 || KS > 1) && idle) return;   // uniform over the workgroup
-  for (int i = tid; i < kDMax + 2; i += 64 * WPG) etab[i] = i <= kDMax ? a.exp_tab[i] : 0;
-  __syncthreads();
-  if (idle) return;   // (no workgroup barrier follows)
+  // the exp table's loads go out first; their LDS stores and the barrier follow the query setup,
+  // so the two memory round trips overlap.  Idle waves (4-wave workgroups) run the setup on a
+  // valid query tile (their own may lie before the first) and leave after the barrier.
+  constexpr int kTabPer = (kDMax + 2 + 64 * WPG - 1) / (64 * WPG);
+  int32_t tabv[kTabPer];
+#pragma unroll
+  for (int j = 0; j < kTabPer; ++j) {
+    const int i = tid + 64 * WPG * j;
+    tabv[j] = i <= kDMax ? a.exp_tab[i] : 0;
+  }
+  if (idle) qt = max(qt, a.q_first >> 5);
 
   const int hh = 3 * kvg + w;
   const int q0 = s0 + 32 * qt, qlast = min(q0 + 31, s0 + T - 1), qi = q0 + c;
@@ -1216,6 +1224,13 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(2))) v
     cq = 128 * sum + (1 << (sh - 1));   // with the rounding offset of RS(., sh)
     __builtin_amdgcn_wave_barrier();
   }
+#pragma unroll
+  for (int j = 0; j < kTabPer; ++j) {
+    const int i = tid + 64 * WPG * j;
+    if (i < kDMax + 2) etab[i] = tabv[j];
+  }
+  __syncthreads();
+  if (idle) return;   // (no workgroup barrier follows)
 
   // K rows of key tile g for this lane (row pi(c) of the tile, d = 32 s + 16 h + 0..15), loaded
   // one tile ahead of their use: int16 values, or with KP their limb bytes (d[s][0] low, d[s][1] high)

@@ -1762,7 +1762,15 @@ __global__ __launch_bounds__(64 * 3 * NW) void attn_decode_kernel(AttnArgs a) {
   int32_t* smax = dsm + kDMax + 1 + 3;                          // [3 NW][4]: each wave's max of each head
   int64_t* sz = (int64_t*)(smax + attn_decode_nmax(NW));        // [3 NW]
   int64_t* spart = sz + 3 * NW;                                 // [12][64]
-  for (int i = tid; i <= kDMax; i += 64 * 3 * NW) etab[i] = a.exp_tab[i];
+  // the exp table's loads go out first and its LDS stores wait until after the scores (before the
+  // first barrier), so the table's memory round trip overlaps the query and key loads
+  constexpr int kTabPer = (kDMax + 1 + 64 * 3 * NW - 1) / (64 * 3 * NW);
+  int32_t tabv[kTabPer];
+#pragma unroll
+  for (int j = 0; j < kTabPer; ++j) {
+    const int i = tid + 64 * 3 * NW * j;
+    if (i <= kDMax) tabv[j] = a.exp_tab[i];
+  }
   const int16_t* base = a.qkv + (size_t)a.seq_off[seq] * kQKVN;   // key 0 of the sequence
   int16_t* const sc_all = (int16_t*)(spart + 3 * NW * 64);      // [3][Lp]
   int32_t* const skl = (int32_t*)(sc_all + 3 * Lp) + 32 * w;     // per wave: 128 sum_d k per key
@@ -1835,6 +1843,11 @@ __global__ __launch_bounds__(64 * 3 * NW) void attn_decode_kernel(AttnArgs a) {
   }
   mxh = max(mxh, __shfl_xor(mxh, 32));
   if (lane < 3) smax[4 * w + lane] = mxh;
+#pragma unroll
+  for (int j = 0; j < kTabPer; ++j) {
+    const int i = tid + 64 * 3 * NW * j;
+    if (i <= kDMax) etab[i] = tabv[j];
+  }
   int16_t* const sc = sc_all + (size_t)hq * Lp;
   // the value rows of this wave's first chunk, loaded now (rows past L re-read row L - 1)
   const int16_t* vcol = base + kD + 192 + kvg * 64 + lane;
